@@ -1,0 +1,177 @@
+// ga_device.hpp -- gfx950 device primitives shared by the HIP kernels.
+//
+// Buffer resources with out-of-range-returns-zero loads, direct-to-LDS
+// 16-byte loads, explicit s_waitcnt, the scaled MFMA, and exact codecs
+// (E4M3 RNE/saturating encode, bf16 RNE). The primitive set follows what
+// the reference's opus.hpp exposes (wmma_opus_rdna4/opus/opus.hpp:1358-1569
+// gmem/async-LDS loads, :1726-1733 waitcnt, :1770-1863 scaled MFMA); the
+// code is written for gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+#include <utility>
+
+namespace ga {
+
+// Compile-time loop: f(std::integral_constant<int, 0>{}) ... f(<N-1>).
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>)
+{
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer resource: base, size in bytes; loads at offset >= size return 0.
+// Word 3 (0x00020000) is the raw-buffer format word for gfx9 parts. Callers
+// pass workgroup-uniform values; readfirstlane makes that visible to the
+// compiler so the descriptor lives in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    const uint64_t up = ((uint64_t)hi << 32) | lo;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)up, (short)0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+
+// 16 bytes per lane from buffer `r` at byte offset voff+soff into LDS at
+// lds_base + lane*16 (lds_base wave-uniform; M0 takes it).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_void* lds_base,
+                                           uint32_t voff, uint32_t soff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
+// s_waitcnt encodings for gfx9: vmcnt[3:0] + vmcnt_hi[15:14], expcnt[6:4],
+// lgkmcnt[11:8]. Only vmcnt is waited on here.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0()
+{
+    __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));
+}
+
+// D = A(16x128) * B(128x16) + C with per-lane E8M0 scales (fp8 operands).
+// Lane l = 16*g + r holds row r: VGPRs 0-3 carry K [16g, 16g+16), VGPRs 4-7
+// carry K [64+16g, 64+16g+16). The scale byte (chosen by OPSEL) of the scale
+// VGPR of lane 16*b + r applies to row r, K [32b, 32b+32). Output: lane l
+// holds D[4*(l/16) + j][l%16], j = 0..3.
+template <int OPSEL_A, int OPSEL_B>
+__device__ __forceinline__ v4f mfma_mx16(v8i a, v8i b, v4f c, int sa, int sb)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, OPSEL_A, sa, OPSEL_B,
+                                                            sb);
+}
+
+// fp32 -> bf16 round to nearest even (quiet NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float x)
+{
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u)
+        return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// OCP E4M3 encode: round to nearest even, saturate to +-448, NaN -> 0x7F.
+__device__ __forceinline__ uint32_t e4m3_encode(float x)
+{
+    uint32_t u = __float_as_uint(x);
+    uint32_t sign = (u >> 24) & 0x80u;
+    uint32_t au = u & 0x7FFFFFFFu;
+    if (au > 0x7F800000u)
+        return 0x7Fu;
+    if (au >= 0x43E00000u) // 448.0f
+        return sign | 0x7Eu;
+    if (au < 0x3C800000u) { // 2^-6: subnormal quantum 2^-9
+        float f = __uint_as_float(au) * 512.0f;
+        uint32_t i = (uint32_t)f;
+        float frac = f - (float)i;
+        if (frac > 0.5f || (frac == 0.5f && (i & 1u)))
+            i++;
+        return sign | i;
+    }
+    int e = (int)(au >> 23) - 127;
+    uint32_t keep = (au >> 20) & 7u, rest = au & 0xFFFFFu;
+    if (rest > 0x80000u || (rest == 0x80000u && (keep & 1u)))
+        keep++;
+    if (keep == 8u) {
+        keep = 0;
+        e++;
+    }
+    uint32_t code = ((uint32_t)(e + 7) << 3) | keep;
+    return sign | (code > 0x7Eu ? 0x7Eu : code);
+}
+
+// Exact floor(log2 a) and 23 fraction bits for a finite a > 0.
+__device__ __forceinline__ void log2_parts(float a, int& E, uint32_t& frac)
+{
+    uint32_t u = __float_as_uint(a) & 0x7FFFFFFFu;
+    int ef = (int)(u >> 23);
+    if (ef > 0) {
+        E = ef - 127;
+        frac = u & 0x7FFFFFu;
+    } else {
+        uint32_t mant = u & 0x7FFFFFu;
+        int msb = 31 - __clz(mant);
+        E = msb - 149;
+        frac = (mant << (23 - msb)) & 0x7FFFFFu;
+    }
+}
+
+// E8M0 exponent of an MX block (rule 0: floor(log2(amax/448)), 1: ceil,
+// 2: OCP floor(log2 amax) - 8). Zero block -> -127.
+__device__ __forceinline__ int mx_scale_exp(float amax, int rule)
+{
+    if (!(amax > 0.0f))
+        return -127;
+    if (__float_as_uint(amax) == 0x7F800000u)
+        return 127;
+    int E;
+    uint32_t f;
+    log2_parts(amax, E, f);
+    int e;
+    if (rule == 0)
+        e = (f >= 0x600000u) ? E - 8 : E - 9;
+    else if (rule == 1)
+        e = (f <= 0x600000u) ? E - 8 : E - 7;
+    else
+        e = E - 8;
+    return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+} // namespace ga

@@ -1,0 +1,56 @@
+// ga_internal.hpp -- host-side internals shared by the library's translation
+// units: error reporting, the compiled kernel registry, workspace handling.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+
+#include "../../include/gcnasm_amd.h"
+
+namespace ga {
+
+// Records a formatted detail message for ga_last_error() and returns `s`.
+ga_status fail(ga_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+ga_status hip_fail(hipError_t e, const char* what);
+
+#define GA_HIP_CHECK(call)                                  \
+    do {                                                    \
+        hipError_t e_ = (call);                             \
+        if (e_ != hipSuccess)                               \
+            return ::ga::hip_fail(e_, #call);               \
+    } while (0)
+
+// One compiled MXFP8 kernel: the manifest row plus its launcher.
+typedef void (*mx_launch_fn)(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy,
+                             int gdz, hipStream_t stream);
+struct MxKernel {
+    ga_tile_config cfg;
+    mx_launch_fn launch;
+};
+int mx_registry_count();
+const MxKernel* mx_registry_get(int idx);
+
+// Library-owned per-device fp32 workspace, grown on demand.
+ga_status default_workspace(size_t bytes, void** ptr);
+
+// Split-K reduce with the MX epilogue folded in:
+//   out[b, m, n] = alpha * sum_s ws[s, b, m, n] (+ bias[n]) (+ beta * c_in[b, m, n])
+// ws is [split_k, batch, padded_M, padded_N]; out/c_in rows are `ldc` elements
+// apart and batches `c_batch_stride` elements apart.
+struct ReduceArgs {
+    const float* ws;
+    void* out;
+    const void* c_in;  // bf16, may be null
+    const void* bias;  // may be null
+    int out_dtype;
+    int bias_dtype;
+    int split_k, M, N, batch, padded_M, padded_N, ldc;
+    long long c_batch_stride;
+    int bias_stride_batch;
+    float alpha, beta;
+};
+ga_status splitk_reduce_launch(const ReduceArgs& a, hipStream_t stream);
+
+} // namespace ga

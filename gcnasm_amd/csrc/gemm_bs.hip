@@ -1,0 +1,344 @@
+// gemm_bs.hip -- FP8 GEMMs with fp32 scales behind the opus_gemm_kargs ABI.
+//
+//   block-scale (DeepSeek):  C[b,m,n] = sum_g P_g[m,n] * SFA[g, m] * SFB(g, n)
+//       P_g = sum over the 128-wide K group g of A*B (fp32 from the MFMA)
+//       SFB(g, n) = SFB[n/128, g] (GROUP_N 128) or SFB[g, n] (GROUP_N 1)
+//       acc = fmaf(P_g, SFA*SFB, acc) per group, in K order
+//       (opus_gemm/block_scale_gemm/README.md:7-26, scale_c_tile in
+//        opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/opus_gemm_utils.cuh:76-96)
+//   per-tensor (fp8_gemm):  C = (sfa[0] * sfb[0]) * sum_k A*B, one fp32 chain
+//
+// A [batch, M, K] and B [batch, N, K] are row-major E4M3 (B is K-major, not
+// preshuffled), K % 128 == 0, M and N arbitrary (rows past M/N load as zero
+// through the buffer range check; a partial last N group of 128 is fine).
+// C is fp32 (the reference's output type) or bf16.
+//
+// Same machinery as the MX kernel: 4 waves, BM x BN tile, K step 128,
+// A and B staged with buffer_load ... lds into the MFMA-order LDS image,
+// v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales (127) and the
+// operands swapped so a lane owns 4 consecutive N of one C row.
+#include "ga_device.hpp"
+#include "ga_internal.hpp"
+
+namespace ga {
+
+enum BsMode { BS_GROUP128 = 0, BS_GROUP1 = 1, BS_TENSOR = 2 };
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int MODE_, int OUT_>
+struct BsCfg {
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr int MODE = MODE_, OUT = OUT_;
+    static constexpr int NT = 256;
+    static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    static constexpr int TM = WTM / 16, TN = WTN / 16;
+    static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int A_LOADS = A_BYTES / (NT * 16);
+    static constexpr int B_LOADS = B_BYTES / (NT * 16);
+    static constexpr int SB_PER_TILE = MODE == BS_GROUP1 ? 4 : 1;
+    static_assert(WAVES_M * WAVES_N == 4, "4 waves");
+    static_assert(A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "tile >= 32 rows");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+constexpr int kBsGroupM = 4;
+
+__device__ __forceinline__ void bs_map_tile(int lin, int gdx, int gdy, int& tm, int& tn)
+{
+    const int total = gdx * gdy;
+    const int full = (total / 8) * 8;
+    if (lin < full)
+        lin = (lin % 8) * (total / 8) + lin / 8;
+    const int per_group = kBsGroupM * gdx;
+    const int g = lin / per_group;
+    const int first_m = g * kBsGroupM;
+    const int gsize = min(gdy - first_m, kBsGroupM);
+    const int r = lin - g * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+template <class C>
+struct BsScales {
+    float sa[C::TM];
+    float sb[C::TN][C::SB_PER_TILE];
+};
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void bs_gemm_kernel(ga_opus_gemm_kargs ka, int tiles_n)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int M = ka.m, N = ka.n, K = ka.k;
+    const int tiles_m = (M + C::BM - 1) / C::BM;
+    int tile_m, tile_n;
+    bs_map_tile(blockIdx.x, tiles_n, tiles_m, tile_m, tile_n);
+    const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
+    const int b = blockIdx.z;
+
+    const char* pa = (const char*)ka.ptr_a + (size_t)b * ka.stride_a_batch + (size_t)m0 * ka.stride_a;
+    const char* pb = (const char*)ka.ptr_b + (size_t)b * ka.stride_b_batch + (size_t)n0 * ka.stride_b;
+    const long long abytes = (long long)(M - m0) * ka.stride_a;
+    const long long bbytes = (long long)(N - n0) * ka.stride_b;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+    uint32_t voff_a[C::A_LOADS], voff_b[C::B_LOADS];
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; i++) {
+        int idx = i * 256 + tid, g = idx >> 7, u = idx & 127;
+        voff_a[i] = (uint32_t)(g * 16 + (u & 15)) * ka.stride_a + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_LOADS; i++) {
+        int idx = i * 256 + tid, g = idx >> 7, u = idx & 127;
+        voff_b[i] = (uint32_t)(g * 16 + (u & 15)) * ka.stride_b + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+    }
+
+    // Scale pointers for this lane's C rows / columns.
+    const float* sfa = (const float*)ka.ptr_sfa + (size_t)b * ka.stride_sfa_batch;
+    const float* sfb = (const float*)ka.ptr_sfb + (size_t)b * ka.stride_sfb_batch;
+    int mrow[C::TM], ncol[C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+        mrow[i] = min(m0 + wm * C::WTM + i * 16 + (lane & 15), M - 1);
+#pragma unroll
+    for (int t = 0; t < C::TN; t++)
+        ncol[t] = n0 + wn * C::WTN + t * 16 + (lane >> 4) * 4;
+
+    auto issue = [&](int buf, int kk) {
+        char* la = smem + buf * C::STAGE;
+        char* lb = la + C::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; i++)
+            lds_load16(ra, (lds_void*)(la + (i * 256 + wave * 64) * 16), voff_a[i] + kk, 0);
+#pragma unroll
+        for (int i = 0; i < C::B_LOADS; i++)
+            lds_load16(rb, (lds_void*)(lb + (i * 256 + wave * 64) * 16), voff_b[i] + kk, 0);
+    };
+    auto load_scales = [&](int g, BsScales<C>& s) {
+        if constexpr (C::MODE != BS_TENSOR) {
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+                s.sa[i] = sfa[(size_t)g * ka.stride_sfa + mrow[i]];
+#pragma unroll
+            for (int t = 0; t < C::TN; t++) {
+                if constexpr (C::MODE == BS_GROUP128) {
+                    int n = min(ncol[t], N - 1);
+                    s.sb[t][0] = sfb[(size_t)(n / 128) * ka.stride_sfb + g];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        s.sb[t][j] = sfb[(size_t)g * ka.stride_sfb + min(ncol[t] + j, N - 1)];
+                }
+            }
+        }
+    };
+
+    v4f acc[C::TM][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int t = 0; t < C::TN; t++)
+            acc[i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int buf, const BsScales<C>& s) {
+        const char* la = smem + buf * C::STAGE;
+        const char* lb = la + C::A_BYTES;
+        const int lo = lane * 16;
+        v8i bf[C::TN];
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            const char* g = lb + (wn * C::TN + t) * 2048 + lo;
+            v4i x0 = *(const v4i*)(g);
+            v4i x1 = *(const v4i*)(g + 1024);
+            bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const char* g = la + (wm * C::TM + i) * 2048 + lo;
+            v4i x0 = *(const v4i*)(g);
+            v4i x1 = *(const v4i*)(g + 1024);
+            v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+            for (int t = 0; t < C::TN; t++) {
+                if constexpr (C::MODE == BS_TENSOR) {
+                    acc[i][t] = mfma_mx16<0, 0>(bf[t], af, acc[i][t], 127, 127);
+                } else {
+                    v4f p = mfma_mx16<0, 0>(bf[t], af, (v4f){0.f, 0.f, 0.f, 0.f}, 127, 127);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float sbv = C::MODE == BS_GROUP128 ? s.sb[t][0] : s.sb[t][j];
+                        float sc = s.sa[i] * sbv;
+                        acc[i][t][j] = __builtin_fmaf(p[j], sc, acc[i][t][j]);
+                    }
+                }
+            }
+        }
+    };
+
+    // K loop: pairs of 128-K steps (stage 0 then stage 1) and an optional
+    // tail step in stage 0. The next stage is issued unconditionally so the
+    // body has no branch: past the last group the LDS loads read in-bounds
+    // bytes that are never used or range-checked zeros, and the scale group
+    // index is clamped to the last group.
+    const int nsteps = K / 128;
+    const int npairs = nsteps >> 1;
+    BsScales<C> cur, nxt;
+    issue(0, 0);
+    load_scales(0, cur);
+    for (int p = 0; p < npairs; p++) {
+        const int s = 2 * p;
+        wait_vmcnt<0>();
+        __syncthreads();
+        issue(1, (s + 1) * 128);
+        load_scales(s + 1, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0, cur);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<0>();
+        __syncthreads();
+        issue(0, (s + 2) * 128);
+        load_scales(min(s + 2, nsteps - 1), cur);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (nsteps & 1) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        compute(0, cur);
+    }
+
+    float tscale = 1.0f;
+    if constexpr (C::MODE == BS_TENSOR)
+        tscale = ((const float*)ka.ptr_sfa)[0] * ((const float*)ka.ptr_sfb)[0];
+
+    char* pc = (char*)ka.ptr_c + (size_t)b * ka.stride_c_batch * (C::OUT == GA_DTYPE_F32 ? 4 : 2);
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
+        const int m = m0 + wm * C::WTM + i * 16 + (lane & 15);
+        if (m >= M)
+            continue;
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            const int n = ncol[t];
+            if (n >= N)
+                continue;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[j] = C::MODE == BS_TENSOR ? acc[i][t][j] * tscale : acc[i][t][j];
+            const size_t off = (size_t)m * ka.stride_c + n;
+            const bool full = n + 4 <= N && (ka.stride_c & 3) == 0;
+            if constexpr (C::OUT == GA_DTYPE_F32) {
+                float* o = (float*)pc + off;
+                if (full)
+                    *(v4f*)o = (v4f){v[0], v[1], v[2], v[3]};
+                else
+                    for (int j = 0; j < 4 && n + j < N; j++)
+                        o[j] = v[j];
+            } else {
+                uint16_t* o = (uint16_t*)pc + off;
+                if (full) {
+                    uint2 pk;
+                    pk.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                    pk.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                    *(uint2*)o = pk;
+                } else {
+                    for (int j = 0; j < 4 && n + j < N; j++)
+                        o[j] = f32_to_bf16(v[j]);
+                }
+            }
+        }
+    }
+}
+
+template <class C>
+static ga_status launch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
+{
+    const int tn = (ka.n + C::BN - 1) / C::BN, tm = (ka.m + C::BM - 1) / C::BM;
+    hipLaunchKernelGGL(bs_gemm_kernel<C>, dim3(tn * tm, 1, ka.batch), dim3(256), 0, stream, ka, tn);
+    GA_HIP_CHECK(hipGetLastError());
+    return GA_OK;
+}
+
+template <int MODE, int OUT>
+static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
+{
+    // The block-scale modes keep the fp32 accumulators in VGPRs (VALU fmaf
+    // per group), so their largest tile is 128x128; the per-tensor mode
+    // accumulates inside the MFMA and takes 256x128.
+    const long long tiles = (long long)((ka.m + 255) / 256) * ((ka.n + 127) / 128) * ka.batch;
+    if (MODE == BS_TENSOR && tiles >= 128)
+        return launch_bs<BsCfg<256, 128, 2, 2, MODE, OUT>>(ka, stream);
+    if (ka.m <= 64)
+        return launch_bs<BsCfg<64, 256, 1, 4, MODE, OUT>>(ka, stream);
+    return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
+}
+
+static ga_status check_kargs(const ga_opus_gemm_kargs* ka)
+{
+    if (!ka || !ka->ptr_a || !ka->ptr_b || !ka->ptr_c || !ka->ptr_sfa || !ka->ptr_sfb)
+        return fail(GA_ERR_ARG, "opus kargs: null pointer");
+    if (ka->m <= 0 || ka->n <= 0 || ka->k <= 0 || ka->batch <= 0)
+        return fail(GA_ERR_ARG, "Invalid problem size: M, N, K and batch must be positive.");
+    if (ka->k % 128 != 0)
+        return fail(GA_ERR_GROUP, "K must be a multiple of GROUP_K (128), got %d", ka->k);
+    if (ka->stride_a < ka->k || ka->stride_b < ka->k || ka->stride_a % 16 || ka->stride_b % 16)
+        return fail(GA_ERR_SHAPE, "stride_a/stride_b must be >= K and multiples of 16");
+    if (ka->stride_c < ka->n)
+        return fail(GA_ERR_SHAPE, "stride_c must be >= N");
+    if (ka->batch > 65535)
+        return fail(GA_ERR_SHAPE, "batch > 65535");
+    return GA_OK;
+}
+
+} // namespace ga
+
+using namespace ga;
+
+extern "C" {
+
+ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype,
+                                  void* stream)
+{
+    ga_status st = check_kargs(kargs);
+    if (st != GA_OK)
+        return st;
+    if (group_n != 128 && group_n != 1)
+        return fail(GA_ERR_ARG, "group_n must be 128 or 1");
+    if (out_dtype != GA_DTYPE_F32 && out_dtype != GA_DTYPE_BF16)
+        return fail(GA_ERR_ARG, "out_dtype must be GA_DTYPE_F32 or GA_DTYPE_BF16");
+    if (group_n == 128 && kargs->stride_sfb < kargs->k / 128)
+        return fail(GA_ERR_SHAPE, "stride_sfb must be >= K/128 for GROUP_N 128");
+    if (group_n == 1 && kargs->stride_sfb < kargs->n)
+        return fail(GA_ERR_SHAPE, "stride_sfb must be >= N for GROUP_N 1");
+    if (kargs->stride_sfa < kargs->m)
+        return fail(GA_ERR_SHAPE, "stride_sfa must be >= M (SFA is [K/128, M])");
+    hipStream_t s = (hipStream_t)stream;
+    if (group_n == 128)
+        return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_GROUP128, GA_DTYPE_F32>(*kargs, s)
+                                         : dispatch_bs<BS_GROUP128, GA_DTYPE_BF16>(*kargs, s);
+    return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_GROUP1, GA_DTYPE_F32>(*kargs, s)
+                                     : dispatch_bs<BS_GROUP1, GA_DTYPE_BF16>(*kargs, s);
+}
+
+ga_status ga_fp8_gemm_per_tensor(const ga_opus_gemm_kargs* kargs, int out_dtype, void* stream)
+{
+    ga_status st = check_kargs(kargs);
+    if (st != GA_OK)
+        return st;
+    if (out_dtype != GA_DTYPE_F32 && out_dtype != GA_DTYPE_BF16)
+        return fail(GA_ERR_ARG, "out_dtype must be GA_DTYPE_F32 or GA_DTYPE_BF16");
+    hipStream_t s = (hipStream_t)stream;
+    return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_TENSOR, GA_DTYPE_F32>(*kargs, s)
+                                     : dispatch_bs<BS_TENSOR, GA_DTYPE_BF16>(*kargs, s);
+}
+
+} // extern "C"

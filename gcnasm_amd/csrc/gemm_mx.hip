@@ -1,0 +1,514 @@
+// gemm_mx.hip -- MXFP8 GEMM for gfx950 behind the f4gemm kernarg ABI.
+//
+//   D[M, N] bf16 = alpha * A[M, K] * B[N, K]^T (+ beta * C)
+//   A, B: OCP E4M3; one E8M0 scale per 1x32 K-block of each row, stored
+//   padded + shuffled (f4gemm_ref.hpp:98-130); B optionally preshuffled in
+//   16x16-byte subtiles (f4gemm_ref.hpp:78-96).
+//
+// Kernel design (gfx950, wave64, 256 threads = 4 waves):
+//  * block tile BM x BN, K step 128; waves in a WAVES_M x WAVES_N grid, each
+//    owning (BM/WAVES_M) x (BN/WAVES_N) of C as 16x16 MFMA tiles.
+//  * A and B are staged in LDS with buffer_load ... lds (16 B per lane,
+//    out-of-range rows read as zero), two stages. The LDS image of every
+//    16-row x 128-K group is 2 KB ordered [K/16:8][row:16][16 B], which is
+//    exactly the preshuffled-B byte order, so B is a linear copy.
+//  * MFMA operand layout of v_mfma_scale_f32_16x16x128_f8f6f4 (fp8): lane
+//    l = 16*g + r holds row r; its VGPRs 0-3 carry K [16g, 16g+16) and VGPRs
+//    4-7 carry K [64+16g, 64+16g+16). So operand half h of every lane is the
+//    1 KB at LDS offset h*1024 + l*16: linear ds_read_b128, no bank conflicts.
+//    The E8M0 scale in lane 16*b + r applies to row r, K [32b, 32b+32).
+//  * v_mfma_scale_f32_16x16x128_f8f6f4 with operands swapped (B rows feed
+//    the MFMA's A side) so each lane ends up with 4 consecutive N outputs of
+//    one C row -> 8-byte bf16 stores.
+//  * The shuffled scale layout puts, for each 32 rows x 256 K, the scales of
+//    lane l (row l%16, K-block l/16) in dword l; the byte inside the dword
+//    (row half, 128-K half) is picked with the MFMA's op_sel.
+//  * Split-K (gdz > 1): each K slice writes fp32 partials to a workspace;
+//    the reduce kernel sums the slices in order and applies the epilogue.
+//  * Tile order: workgroup ids are dispatched round-robin over the 8 XCDs;
+//    they are remapped so each XCD works on a contiguous, M-grouped range of
+//    tiles and shares A/B panels in its own L2.
+#include "ga_device.hpp"
+#include "ga_internal.hpp"
+
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace ga {
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, bool BPS_>
+struct MxCfg {
+    static constexpr int BM = BM_, BN = BN_;
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr bool BPS = BPS_;
+    static constexpr int NT = 256;
+    static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    static constexpr int TM = WTM / 16, TN = WTN / 16;
+    static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int A_LOADS = A_BYTES / (NT * 16);
+    static constexpr int B_LOADS = B_BYTES / (NT * 16);
+    static_assert(WAVES_M * WAVES_N == 4, "4 waves");
+    // 32-aligned wave tiles: the row half of each 16-row MFMA tile inside a
+    // 32-row scale block is (tile index & 1), known at compile time.
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile multiple of 32");
+    static_assert(A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "tile >= 32 rows");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+};
+
+constexpr int kGroupM = 4; // M-tiles per L2 group
+
+// Workgroup (x, y) -> (tile_m, tile_n): XCD-contiguous ranges, then column
+// sweeps inside groups of kGroupM M-tiles.
+__device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int& tm, int& tn)
+{
+    const int total = gdx * gdy;
+    int lin = by * gdx + bx;
+    const int full = (total / 8) * 8;
+    if (lin < full)
+        lin = (lin % 8) * (total / 8) + lin / 8;
+    const int per_group = kGroupM * gdx;
+    const int g = lin / per_group;
+    const int first_m = g * kGroupM;
+    const int gsize = min(gdy - first_m, kGroupM);
+    const int r = lin - g * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+template <class C>
+struct MxState {
+    __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
+    uint32_t voff_a[C::A_LOADS];
+    uint32_t voff_b[C::B_LOADS];
+    uint32_t soff_a[C::TM]; // scale dword byte offset of each A row tile (group 0)
+    uint32_t soff_b[C::TN];
+    uint32_t b_kstride; // bytes per K step of 128 in B
+};
+
+template <class C>
+__device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, int buf, int kk,
+                                            int wave)
+{
+    char* sa = smem + buf * C::STAGE;
+    char* sb = sa + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; i++)
+        lds_load16(st.ra, (lds_void*)(sa + (i * 256 + wave * 64) * 16), st.voff_a[i] + kk, 0);
+#pragma unroll
+    for (int i = 0; i < C::B_LOADS; i++)
+        lds_load16(st.rb, (lds_void*)(sb + (i * 256 + wave * 64) * 16),
+                   st.voff_b[i] + (uint32_t)(kk / 128) * st.b_kstride, 0);
+}
+
+template <class C>
+__device__ __forceinline__ void load_scales(const MxState<C>& st, int q, uint32_t (&sa)[C::TM],
+                                            uint32_t (&sb)[C::TN])
+{
+    // q-th group of 256 K; consecutive groups are 256 bytes apart.
+#pragma unroll
+    for (int t = 0; t < C::TM; t++)
+        sa[t] = buf_load4(st.rsa, st.soff_a[t] + q * 256, 0);
+#pragma unroll
+    for (int t = 0; t < C::TN; t++)
+        sb[t] = buf_load4(st.rsb, st.soff_b[t] + q * 256, 0);
+}
+
+template <class C, int PAR>
+__device__ __forceinline__ void compute_stage(const char* smem, int buf, int wm, int wn, int lane,
+                                              const uint32_t (&sa)[C::TM],
+                                              const uint32_t (&sb)[C::TN],
+                                              v4f (&acc)[C::TM][C::TN])
+{
+    const char* la = smem + buf * C::STAGE;
+    const char* lb = la + C::A_BYTES;
+    const int lo = lane * 16;
+    v8i bf[C::TN];
+#pragma unroll
+    for (int t = 0; t < C::TN; t++) {
+        const char* g = lb + (wn * C::TN + t) * 2048 + lo;
+        v4i x0 = *(const v4i*)(g);
+        v4i x1 = *(const v4i*)(g + 1024);
+        bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    }
+    static_for<C::TM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        const char* g = la + (wm * C::TM + i) * 2048 + lo;
+        v4i x0 = *(const v4i*)(g);
+        v4i x1 = *(const v4i*)(g + 1024);
+        v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        static_for<C::TN>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            // op_sel picks byte (128-K half, 16-row half) of the scale dword
+            acc[i][t] = mfma_mx16<PAR * 2 + (t & 1), PAR * 2 + (i & 1)>(bf[t], af, acc[i][t],
+                                                                      (int)sb[t], (int)sa[i]);
+        });
+    });
+}
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+    int tile_m, tile_n;
+    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, tile_m, tile_n);
+    const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
+
+    const int z = blockIdx.z, gdz = gridDim.z;
+    int kpt = K;
+    if (gdz > 1)
+        kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
+    const int kb = z * kpt;
+    const int ke = min(K, kb + kpt);
+    const int nsteps = (ke - kb) / 128;
+
+    const uint32_t lda = args.stride_A0, ldb = args.stride_B0;
+    const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
+
+    MxState<C> st;
+    {
+        const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
+        long long abytes = (long long)(M - m0) * lda;
+        st.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; i++) {
+            int idx = i * 256 + tid;
+            int g = idx >> 7, u = idx & 127;
+            int row = g * 16 + (u & 15);
+            st.voff_a[i] = (uint32_t)row * lda + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+        }
+        if (C::BPS) {
+            const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
+            long long bbytes = (long long)(N - n0) * K;
+            st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+            st.b_kstride = 128 * 16;
+#pragma unroll
+            for (int i = 0; i < C::B_LOADS; i++) {
+                int idx = i * 256 + tid;
+                int g = idx >> 7, u = idx & 127;
+                st.voff_b[i] = (uint32_t)g * (uint32_t)K * 16 + (uint32_t)u * 16;
+            }
+        } else {
+            const char* pb = (const char*)args.ptr_B + (size_t)n0 * ldb;
+            long long bbytes = (long long)(N - n0) * ldb;
+            st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+            st.b_kstride = 128;
+#pragma unroll
+            for (int i = 0; i < C::B_LOADS; i++) {
+                int idx = i * 256 + tid;
+                int g = idx >> 7, u = idx & 127;
+                int row = g * 16 + (u & 15);
+                st.voff_b[i] = (uint32_t)row * ldb + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+            }
+        }
+        // Scales: shuffled layout, 256-byte block per (32 rows, 256 K).
+        const int sma = (M + 31) / 32 * 32, smb = (N + 31) / 32 * 32;
+        st.rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)sma * sna);
+        st.rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)smb * snb);
+        const int q0 = kb / 256;
+#pragma unroll
+        for (int t = 0; t < C::TM; t++) {
+            int r = m0 + wm * C::WTM + t * 16;
+            st.soff_a[t] = ((uint32_t)(r / 32) * (sna / 8) + q0) * 256 + lane * 4;
+        }
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            int r = n0 + wn * C::WTN + t * 16;
+            st.soff_b[t] = ((uint32_t)(r / 32) * (snb / 8) + q0) * 256 + lane * 4;
+        }
+    }
+
+    v4f acc[C::TM][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int t = 0; t < C::TN; t++)
+            acc[i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    // K loop: pairs of 128-K steps (one 256-K scale group per pair, stage 0
+    // then stage 1), then an optional single tail step in stage 0.
+    uint32_t sa[C::TM], sb[C::TN], na[C::TM], nb[C::TN];
+    const int npairs = nsteps >> 1;
+    if (nsteps > 0) {
+        issue_stage<C>(st, smem, 0, kb, wave);
+        load_scales<C>(st, 0, sa, sb);
+    }
+    for (int p = 0; p < npairs; p++) {
+        const int s = 2 * p;
+        wait_vmcnt<0>();
+        __syncthreads();
+        issue_stage<C>(st, smem, 1, kb + (s + 1) * 128, wave);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_stage<C, 0>(smem, 0, wm, wn, lane, sa, sb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<0>();
+        __syncthreads();
+        // Issued unconditionally to keep the loop body branch-free: on the
+        // last pair this prefetches the tail step, or re-reads in-bounds
+        // bytes past the slice (never used), and range-checked loads past
+        // the end of A, B or a scale buffer return zero.
+        issue_stage<C>(st, smem, 0, kb + (s + 2) * 128, wave);
+        load_scales<C>(st, p + 1, na, nb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_stage<C, 1>(smem, 1, wm, wn, lane, sa, sb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < C::TM; t++)
+            sa[t] = na[t];
+#pragma unroll
+        for (int t = 0; t < C::TN; t++)
+            sb[t] = nb[t];
+    }
+    if (nsteps & 1) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        compute_stage<C, 0>(smem, 0, wm, wn, lane, sa, sb, acc);
+    }
+
+    // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile. The library is
+    // built with -ffp-contract=off: alpha*v and + beta*c round separately.
+    const int ldd = (int)args.stride_C0;
+    const float alpha = args.alpha, beta = args.beta;
+    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
+        const int m = m0 + wm * C::WTM + i * 16 + (lane & 15);
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            const int n = n0 + wn * C::WTN + t * 16 + (lane >> 4) * 4;
+            if (m >= M || n >= N)
+                continue;
+            v4f v = acc[i][t];
+            if (gdz > 1) {
+                *(v4f*)(ws + ((size_t)z * M + m) * N + n) = v;
+            } else {
+                uint16_t o[4];
+                const uint16_t* cin = use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n
+                                            : nullptr;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float r = alpha * v[j];
+                    if (use_c)
+                        r = r + beta * bf16_to_f32(cin[j]);
+                    o[j] = f32_to_bf16(r);
+                }
+                uint2 pk;
+                pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+            }
+        }
+    }
+}
+
+template <class C>
+static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                      hipStream_t stream)
+{
+    hipLaunchKernelGGL(mx_gemm_kernel<C>, dim3(gdx, gdy, gdz), dim3(256), 0, stream, args, ws);
+}
+
+#define GA_MX_ENTRY(BM, BN, WGM, WGN, BPS, SPLIT, SUFFIX)                                      \
+    {{BM, BN, SPLIT, BPS,                                                                     \
+      "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
+      "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0)>>}
+#define GA_BPS_NAME_1 "BpreShuffle"
+#define GA_BPS_NAME_0 "noBpreShuffle"
+
+// Manifest order matters: the heuristic breaks ties by it.
+static const MxKernel g_mx_kernels[] = {
+    GA_MX_ENTRY(256, 128, 2, 2, 1, 0, ""),
+    GA_MX_ENTRY(128, 256, 2, 2, 1, 0, ""),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 0, ""),
+    GA_MX_ENTRY(64, 256, 1, 4, 1, 0, ""),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 0, ""),
+    GA_MX_ENTRY(256, 128, 2, 2, 1, 1, "_splitK"),
+    GA_MX_ENTRY(128, 256, 2, 2, 1, 1, "_splitK"),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 1, "_splitK"),
+    GA_MX_ENTRY(64, 256, 1, 4, 1, 1, "_splitK"),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 1, "_splitK"),
+    GA_MX_ENTRY(32, 512, 1, 4, 1, 1, "_splitK"),
+    GA_MX_ENTRY(256, 128, 2, 2, 0, 0, ""),
+    GA_MX_ENTRY(128, 128, 2, 2, 0, 1, "_splitK"),
+};
+
+int mx_registry_count() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
+const MxKernel* mx_registry_get(int idx) { return &g_mx_kernels[idx]; }
+
+ga_status default_workspace(size_t bytes, void** ptr)
+{
+    static std::mutex mu;
+    static std::vector<std::pair<void*, size_t>> per_dev;
+    std::lock_guard<std::mutex> lock(mu);
+    int dev = 0;
+    GA_HIP_CHECK(hipGetDevice(&dev));
+    if ((int)per_dev.size() <= dev)
+        per_dev.resize(dev + 1, {nullptr, 0});
+    auto& slot = per_dev[dev];
+    if (slot.second < bytes) {
+        if (slot.first) {
+            GA_HIP_CHECK(hipDeviceSynchronize());
+            GA_HIP_CHECK(hipFree(slot.first));
+            slot = {nullptr, 0};
+        }
+        void* p = nullptr;
+        GA_HIP_CHECK(hipMalloc(&p, bytes));
+        slot = {p, bytes};
+    }
+    *ptr = slot.first;
+    return GA_OK;
+}
+
+} // namespace ga
+
+using namespace ga;
+
+extern "C" {
+
+ga_status ga_kernel_find(const char* name, int* idx)
+{
+    if (!name || !idx)
+        return fail(GA_ERR_ARG, "null argument");
+    for (int i = 0; i < mx_registry_count(); i++) {
+        const ga_tile_config& c = g_mx_kernels[i].cfg;
+        if (!strcmp(c.knl_name, name) || !strcmp(c.co_name, name)) {
+            *idx = i;
+            return GA_OK;
+        }
+    }
+    *idx = -1;
+    return fail(GA_ERR_NO_KERNEL, "kernel '%s' not in the manifest", name);
+}
+
+size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N)
+{
+    (void)idx;
+    if (!ld || ld->gdz <= 1 || M <= 0 || N <= 0)
+        return 0;
+    return (size_t)ld->gdz * M * N * sizeof(float);
+}
+
+ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
+                           void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (!args || idx < 0 || idx >= mx_registry_count())
+        return fail(GA_ERR_ARG, "kernel_launch: bad kernel index %d", idx);
+    const MxKernel& k = g_mx_kernels[idx];
+    const int M = (int)args->M, N = (int)args->N, K = (int)args->K;
+    if (M <= 0 || N <= 0 || K <= 0 || !args->ptr_A || !args->ptr_B || !args->ptr_D ||
+        !args->ptr_ScaleA || !args->ptr_ScaleB)
+        return fail(GA_ERR_ARG, "kernel_launch: null pointer or empty shape");
+    if (K % 128 != 0)
+        return fail(GA_ERR_SHAPE, "K must be a multiple of 128 (got %d)", K);
+    if (N % 16 != 0)
+        return fail(GA_ERR_SHAPE, "N must be a multiple of 16 (got %d)", N);
+    if (args->stride_C0 % 4 != 0 || args->stride_C0 < (uint32_t)N)
+        return fail(GA_ERR_SHAPE, "stride_C0 must be >= N and a multiple of 4 (got %u)",
+                    args->stride_C0);
+    if (args->stride_A0 % 16 != 0 || args->stride_A0 < (uint32_t)K ||
+        (!k.cfg.bpreshuffle && (args->stride_B0 % 16 != 0 || args->stride_B0 < (uint32_t)K)))
+        return fail(GA_ERR_SHAPE, "A/B row strides must be >= K and multiples of 16");
+    if (args->stride_ScaleA0 < (uint32_t)(K / 32) || args->stride_ScaleA0 % 8 ||
+        args->stride_ScaleB0 < (uint32_t)(K / 32) || args->stride_ScaleB0 % 8)
+        return fail(GA_ERR_SHAPE, "scale strides must be the padded column count "
+                                  "round_up(K/32, 8)");
+    if (gdx != (N + k.cfg.tile_N - 1) / k.cfg.tile_N || gdy != (M + k.cfg.tile_M - 1) / k.cfg.tile_M ||
+        gdz < 1)
+        return fail(GA_ERR_ARG, "grid (%d,%d,%d) does not match tile %dx%d", gdx, gdy, gdz,
+                    k.cfg.tile_M, k.cfg.tile_N);
+    if (gdz > 1) {
+        int L = args->log2_k_split;
+        if (L < 0 || L > 30 || K % (1 << L) != 0)
+            return fail(GA_ERR_SPLITK, "bad log2_k_split %d for K=%d", L, K);
+        int kpt = ((K >> L) + 255) / 256 * 256;
+        if ((K + kpt - 1) / kpt != gdz)
+            return fail(GA_ERR_ARG, "gdz=%d does not match log2_k_split=%d", gdz, L);
+    }
+    hipStream_t s = (hipStream_t)stream;
+    float* ws = nullptr;
+    if (gdz > 1) {
+        size_t need = (size_t)gdz * M * N * sizeof(float);
+        if (workspace) {
+            if (workspace_bytes < need)
+                return fail(GA_ERR_WORKSPACE, "workspace %zu bytes, need %zu", workspace_bytes,
+                            need);
+            ws = (float*)workspace;
+        } else {
+            void* p = nullptr;
+            ga_status st = default_workspace(need, &p);
+            if (st != GA_OK)
+                return st;
+            ws = (float*)p;
+        }
+    }
+    k.launch(*args, ws, gdx, gdy, gdz, s);
+    GA_HIP_CHECK(hipGetLastError());
+    if (gdz > 1) {
+        ReduceArgs r;
+        r.ws = ws;
+        r.out = args->ptr_D;
+        r.c_in = (args->beta != 0.0f) ? args->ptr_C : nullptr;
+        r.bias = nullptr;
+        r.out_dtype = GA_DTYPE_BF16;
+        r.bias_dtype = GA_DTYPE_F32;
+        r.split_k = gdz;
+        r.M = M;
+        r.N = N;
+        r.batch = 1;
+        r.padded_M = M;
+        r.padded_N = N;
+        r.ldc = (int)args->stride_C0;
+        r.c_batch_stride = 0;
+        r.bias_stride_batch = 0;
+        r.alpha = args->alpha;
+        r.beta = args->beta;
+        return splitk_reduce_launch(r, s);
+    }
+    return GA_OK;
+}
+
+ga_status ga_mxfp8_gemm(void* d_D, const void* d_A, const void* d_B, const void* d_ScaleA,
+                        const void* d_ScaleB, int M, int N, int K, int stride_D0,
+                        int bpreshuffle, int log2_k_split, int num_cu, void* workspace,
+                        size_t workspace_bytes, int* chosen, ga_launch_desc* ld_out,
+                        void* stream)
+{
+    if (num_cu <= 0) {
+        ga_status st = ga_device_num_cu(&num_cu);
+        if (st != GA_OK)
+            return st;
+    }
+    int idx = -1, l2 = 0;
+    ga_status st = ga_select_kernel(M, N, K, num_cu, log2_k_split, bpreshuffle, nullptr, 0,
+                                    &idx, &l2);
+    if (st != GA_OK)
+        return st;
+    ga_launch_desc ld;
+    st = ga_make_launch(&g_mx_kernels[idx].cfg, M, N, K, l2, &ld);
+    if (st != GA_OK)
+        return st;
+    ga_mx_shape sh;
+    st = ga_mx_shape_init(M, N, K, 8, &sh);
+    if (st != GA_OK)
+        return st;
+    ga_f4gemm_kargs args;
+    ga_fill_args(&args, d_D, nullptr, (void*)d_A, (void*)d_B, (void*)d_ScaleA, (void*)d_ScaleB,
+                 M, N, K, stride_D0, sh.scale_cols, sh.scale_cols, 1.0f, 0.0f, ld.log2_k_split);
+    if (chosen)
+        *chosen = idx;
+    if (ld_out)
+        *ld_out = ld;
+    return ga_kernel_launch(idx, &args, ld.gdx, ld.gdy, ld.gdz, workspace, workspace_bytes,
+                            stream);
+}
+
+} // extern "C"

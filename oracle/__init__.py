@@ -1,0 +1,303 @@
+"""Python binding of the CPU oracle (oracle/liboracle.so) and of oracle/_ref.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the gcnasm_amd package.
+
+  O = load()       the oracle (plain-C restatement of the reference path)
+  R = load_ref()   the reference's own header-only CPU code (asm_f4gemm/
+                   f4gemm.hpp and f4gemm_ref.hpp) compiled in place; None when
+                   it was not built (no reference tree available)
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libgcnasm_ref.so")
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_u8 = ctypes.c_uint8
+_u16 = ctypes.c_uint16
+_sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
+
+_SIGS = {
+    "or_e4m3_encode": (_u8, [_f]),
+    "or_e4m3_decode": (_f, [_u8]),
+    "or_e8m0_to_f32": (_f, [_u8]),
+    "or_f32_to_bf16": (_u16, [_f]),
+    "or_bf16_to_f32": (_f, [_u16]),
+    "or_fp4_decode": (_f, [_u8]),
+    "or_floor_log2": (_i, [_f]),
+    "or_mx_scale_exp": (_i, [_f, _i]),
+    "or_quant_mxfp8": (None, [_vp, _i, _i, _vp, _vp, _i]),
+    "or_quant_fp8_1x128": (None, [_vp, _i, _i, _vp, _vp]),
+    "or_quant_fp8_128x128": (None, [_vp, _i, _i, _vp, _vp]),
+    "or_quant_fp8_per_tensor": (None, [_vp, _sz, _vp, _vp]),
+    "or_shuffle_weight_16x16": (None, [_vp, _vp, _i, _i]),
+    "or_shuffle_scale": (None, [_vp, _vp, _i, _i, _i, _i]),
+    "or_select_kernel": (_i, [_i, _i, _i, _i, _i, _i, _vp, _i, ctypes.POINTER(_i)]),
+    "or_make_launch": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                            ctypes.POINTER(_i), ctypes.POINTER(_i)]),
+    "or_reference_gemm": (None, [_vp, _vp, _i, _i, _i, _f, _vp]),
+    "or_gemm_mxfp8_exact": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "or_gemm_mxfp8_fp32acc": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    "or_gemm_blockscale_ref": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
+                                      _i, _i]),
+    "or_gemm_blockscale_fp32acc": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                                          _i, _i, _i]),
+    "or_gemm_blockscale_exact": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i]),
+    "or_gemm_per_tensor_fp32acc": (None, [_vp, _vp, _f, _f, _vp, _i, _i, _i]),
+    "or_splitk_reduce": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i]),
+    "or_randn": (None, [_vp, _sz, _u64, _f, _f]),
+    "or_gen_mx_input": (None, [_vp, _i, _i, _u64, _f, _i]),
+}
+
+_REF_SIGS = {
+    "ref_shuffle_weight_16x16": (None, [_vp, _vp, _i, _i]),
+    "ref_shuffle_scale": (None, [_vp, _vp, _i, _i, _i, _i]),
+    "ref_e8m0_to_f32": (_f, [_u8]),
+    "ref_bf16_to_f32": (_f, [_u16]),
+    "ref_fp4_lut": (_f, [_i]),
+    "ref_reference_gemm": (None, [_vp, _vp, _i, _i, _i, _f, _vp]),
+    "ref_select_kernel": (_i, [_i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i,
+                               ctypes.POINTER(_i)]),
+    "ref_make_launch": (None, [_i, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "ref_kernelargs_size": (_i, []),
+    "ref_threads": (_i, [_i]),
+    "ref_fill_args": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _f,
+                             _i]),
+    "ref_load_configs": (_i, [ctypes.c_char_p, _vp, _vp, _vp, _vp, _i]),
+    "ref_shape": (None, [_i, _i, _i, _vp]),
+    "ref_make_operand": (None, [_i, _i, ctypes.c_uint32, _vp, _vp, _vp]),
+}
+
+
+def _bind(path, sigs):
+    lib = ctypes.CDLL(path)
+    for n, (r, a) in sigs.items():
+        fn = getattr(lib, n)
+        fn.restype = r
+        fn.argtypes = a
+    return lib
+
+
+_O = None
+_R = None
+
+
+def load():
+    global _O
+    if _O is None:
+        if not os.path.exists(LIB):
+            raise ImportError("oracle/liboracle.so not built: make -C oracle")
+        _O = _bind(LIB, _SIGS)
+    return _O
+
+
+def load_ref():
+    global _R
+    if _R is None and os.path.exists(REF_LIB):
+        _R = _bind(REF_LIB, _REF_SIGS)
+    return _R
+
+
+def p(a):
+    """ctypes pointer of a C-contiguous numpy array."""
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ---- numpy-level helpers ---------------------------------------------------
+def randn(n, seed, mean=0.0, std=1.0):
+    out = np.empty(n, dtype=np.float32)
+    load().or_randn(p(out), n, seed, mean, std)
+    return out
+
+
+def gen_mx_input(rows, K, seed, std=1.0, spread=4):
+    x = np.empty((rows, K), dtype=np.float32)
+    load().or_gen_mx_input(p(x), rows, K, seed, std, spread)
+    return x
+
+
+def quant_mxfp8(x, rule=0):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), dtype=np.uint8)
+    s = np.empty((rows, K // 32), dtype=np.uint8)
+    load().or_quant_mxfp8(p(x), rows, K, p(q), p(s), rule)
+    return q, s
+
+
+def quant_fp8_1x128(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), dtype=np.uint8)
+    s = np.empty((K // 128, rows), dtype=np.float32)
+    load().or_quant_fp8_1x128(p(x), rows, K, p(q), p(s))
+    return q, s
+
+
+def quant_fp8_128x128(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K), dtype=np.uint8)
+    s = np.empty(((rows + 127) // 128, K // 128), dtype=np.float32)
+    load().or_quant_fp8_128x128(p(x), rows, K, p(q), p(s))
+    return q, s
+
+
+def quant_fp8_per_tensor(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.shape, dtype=np.uint8)
+    s = np.empty((1,), dtype=np.float32)
+    load().or_quant_fp8_per_tensor(p(x), x.size, p(q), p(s))
+    return q, s
+
+
+def shuffle_weight_16x16(src, N, Kp):
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty(N * Kp, dtype=np.uint8)
+    load().or_shuffle_weight_16x16(p(src), p(dst), N, Kp)
+    return dst
+
+
+def shuffle_scale(src, rows, cols, sm, sn):
+    src = np.ascontiguousarray(src, dtype=np.uint8)
+    dst = np.empty(sm * sn, dtype=np.uint8)
+    load().or_shuffle_scale(p(src), p(dst), rows, cols, sm, sn)
+    return dst
+
+
+def e4m3_decode_table():
+    O = load()
+    return np.array([O.or_e4m3_decode(c) for c in range(256)], dtype=np.float32)
+
+
+def e8m0_decode_table():
+    O = load()
+    return np.array([O.or_e8m0_to_f32(c) for c in range(256)], dtype=np.float32)
+
+
+def mx_dequant(q, s):
+    """f64 values of an MX operand (q [rows, K] codes, s [rows, K/32] E8M0)."""
+    t = e4m3_decode_table().astype(np.float64)
+    sc = e8m0_decode_table().astype(np.float64)
+    return t[q] * np.repeat(sc[s], 32, axis=1)
+
+
+def mx_absdot(qa, sa, qb, sb):
+    """sum_k |a_k * b_k| per output (dequantised, f64): the magnitude that bounds
+    the MFMA's internal truncation error."""
+    return np.abs(mx_dequant(qa, sa)) @ np.abs(mx_dequant(qb, sb)).T
+
+
+def fp8_absdot(qa, qb):
+    t = np.abs(e4m3_decode_table().astype(np.float64))
+    return t[qa] @ t[qb].T
+
+
+def blockscale_absdot(qa, qb, sfa, sfb, group_n=128):
+    """sum_g |sa*sb| * sum_{k in g} |a_k b_k| per output."""
+    t = np.abs(e4m3_decode_table().astype(np.float64))
+    A, B = t[qa], t[qb]
+    M, K = qa.shape
+    N = qb.shape[0]
+    out = np.zeros((M, N))
+    for g in range(K // 128):
+        pg = A[:, g * 128:(g + 1) * 128] @ B[:, g * 128:(g + 1) * 128].T
+        sa = np.abs(sfa[g, :M].astype(np.float64))[:, None]
+        if group_n == 128:
+            sb = np.abs(sfb[np.arange(N) // 128, g].astype(np.float64))[None, :]
+        else:
+            sb = np.abs(sfb[g, :N].astype(np.float64))[None, :]
+        out += pg * sa * sb
+    return out
+
+
+def gemm_mxfp8_exact(qa, sa, qb, sb):
+    M, K = qa.shape
+    N = qb.shape[0]
+    D = np.empty((M, N), dtype=np.float64)
+    load().or_gemm_mxfp8_exact(p(np.ascontiguousarray(qa)), p(np.ascontiguousarray(qb)),
+                               p(np.ascontiguousarray(sa)), p(np.ascontiguousarray(sb)), M, N,
+                               K, p(D))
+    return D
+
+
+def gemm_mxfp8_fp32acc(qa, sa, qb, sb, log2_k_split=0, alpha=1.0):
+    M, K = qa.shape
+    N = qb.shape[0]
+    D = np.empty((M, N), dtype=np.float32)
+    load().or_gemm_mxfp8_fp32acc(p(np.ascontiguousarray(qa)), p(np.ascontiguousarray(qb)),
+                                 p(np.ascontiguousarray(sa)), p(np.ascontiguousarray(sb)), M,
+                                 N, K, log2_k_split, alpha, p(D))
+    return D
+
+
+def _sfb_stride(N, K, group_n):
+    return K // 128 if group_n == 128 else N
+
+
+def gemm_blockscale_ref(qa, qb, sfa, sfb, group_n=128):
+    M, K = qa.shape
+    N = qb.shape[0]
+    C = np.empty((M, N), dtype=np.float32)
+    load().or_gemm_blockscale_ref(p(qa), p(qb), p(sfa), p(sfb), p(C), M, N, K, K, K, N, M,
+                                  _sfb_stride(N, K, group_n), group_n)
+    return C
+
+
+def gemm_blockscale_fp32acc(qa, qb, sfa, sfb, group_n=128):
+    M, K = qa.shape
+    N = qb.shape[0]
+    C = np.empty((M, N), dtype=np.float32)
+    load().or_gemm_blockscale_fp32acc(p(qa), p(qb), p(sfa), p(sfb), p(C), M, N, K, K, K, N, M,
+                                      _sfb_stride(N, K, group_n), group_n)
+    return C
+
+
+def gemm_blockscale_exact(qa, qb, sfa, sfb, group_n=128):
+    M, K = qa.shape
+    N = qb.shape[0]
+    C = np.empty((M, N), dtype=np.float64)
+    load().or_gemm_blockscale_exact(p(qa), p(qb), p(sfa), p(sfb), p(C), M, N, K, M,
+                                    _sfb_stride(N, K, group_n), group_n)
+    return C
+
+
+def gemm_per_tensor_fp32acc(qa, qb, sa, sb):
+    M, K = qa.shape
+    N = qb.shape[0]
+    C = np.empty((M, N), dtype=np.float32)
+    load().or_gemm_per_tensor_fp32acc(p(qa), p(qb), float(sa), float(sb), p(C), M, N, K)
+    return C
+
+
+def reference_gemm(A, B, alpha=1.0):
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    B = np.ascontiguousarray(B, dtype=np.float32)
+    M, K = A.shape
+    N = B.shape[0]
+    D = np.empty((M, N), dtype=np.float32)
+    load().or_reference_gemm(p(A), p(B), M, N, K, alpha, p(D))
+    return D
+
+
+def to_bf16_bits(x):
+    """fp32 array -> uint16 bf16 bits (RNE), via the oracle's rounding."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, ((u >> 16) | 0x40) & 0xFFFF, r)
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)

@@ -1,0 +1,598 @@
+/*
+ * oracle.c -- CPU restatement of the reference's block-scaled FP8 GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). Built with -O2 -ffp-contract=off
+ * and without -ffast-math, so every fp32 operation below rounds exactly once
+ * in the order written.
+ *
+ * How each part is pinned (tests/test_oracle_*.py):
+ *   e4m3 encode/decode   exhaustive vs ROCm's host __hip_fp8_e4m3 and vs
+ *                        torch.float8_e4m3fn (after a clamp to +-448)
+ *   e8m0 decode          vs the reference's own e8m0_to_f32 compiled from
+ *                        /root/reference (oracle/_ref) and torch float8_e8m0fnu
+ *   bf16                 vs torch .to(bfloat16) (RNE) on random + edge bits
+ *   mx scale rules       closed-form invariants on amax/2^e
+ *   quantisers           brute-force nearest-code search over all 256 codes
+ *   shuffles             vs the reference's shuffle functions (oracle/_ref)
+ *                        and vs the documented view/permute in numpy
+ *   select/make_launch   vs the reference's f4gemm.hpp (oracle/_ref)
+ *   GEMMs                vs the reference's reference_gemm (oracle/_ref), vs
+ *                        numpy float64 matmul, and vs each other
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------- */
+/* E4M3 (OCP "fn" flavour used by gfx950): bias 7, no inf, NaN = S.1111.111,  */
+/* max finite 0x7E = 448, min subnormal 2^-9. opus.hpp:858-871 describes the  */
+/* gfx950 value set (max 0x7E, NaN 0x7F).                                     */
+/* ------------------------------------------------------------------------- */
+float or_e4m3_decode(uint8_t c)
+{
+    int s = c >> 7, e = (c >> 3) & 0xF, m = c & 7;
+    float v;
+    if (e == 15 && m == 7)
+        return u2f(0x7FC00000u);
+    if (e == 0)
+        v = ldexpf((float)m, -9);
+    else
+        v = ldexpf((float)(8 + m), e - 10);
+    return s ? -v : v;
+}
+
+uint8_t or_e4m3_encode(float x)
+{
+    uint32_t u = f2u(x);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+    uint32_t au = u & 0x7FFFFFFFu;
+    if (au > 0x7F800000u)
+        return 0x7F; /* NaN */
+    float a = u2f(au);
+    if (a >= 448.0f)
+        return sign | 0x7E; /* SATFINITE, also for +-inf */
+    if (a < 0.015625f) {
+        /* subnormal range: quantum 2^-9; a*512 is exact */
+        float f = a * 512.0f;
+        int i = (int)f;
+        float frac = f - (float)i;
+        if (frac > 0.5f || (frac == 0.5f && (i & 1)))
+            i++;
+        return sign | (uint8_t)i; /* i == 8 is the min normal 0x08 */
+    }
+    int e = (int)((au >> 23) & 0xFF) - 127; /* -6 .. 8 */
+    uint32_t mant = au & 0x7FFFFFu;
+    uint32_t keep = mant >> 20, rest = mant & 0xFFFFFu;
+    if (rest > 0x80000u || (rest == 0x80000u && (keep & 1)))
+        keep++;
+    if (keep == 8) {
+        keep = 0;
+        e++;
+    }
+    uint32_t code = ((uint32_t)(e + 7) << 3) | keep;
+    if (code > 0x7E)
+        code = 0x7E;
+    return sign | (uint8_t)code;
+}
+
+/* f4gemm_ref.hpp:29-41: value 2^(e-127); e == 0 -> bits 0x00400000; 0xFF -> NaN. */
+float or_e8m0_to_f32(uint8_t e)
+{
+    uint32_t bits;
+    if (e == 0)
+        bits = 0x00400000u;
+    else if (e == 0xFF)
+        bits = 0x7F800001u;
+    else
+        bits = (uint32_t)e << 23;
+    return u2f(bits);
+}
+
+/* bf16 round-to-nearest-even (opus.hpp:944-950); NaN stays a quiet NaN. */
+uint16_t or_f32_to_bf16(float x)
+{
+    uint32_t u = f2u(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u)
+        return (uint16_t)((u >> 16) | 0x40);
+    uint32_t lsb = (u >> 16) & 1u;
+    u += 0x7FFFu + lsb;
+    return (uint16_t)(u >> 16);
+}
+
+float or_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+/* kFp4Lut (f4gemm_ref.hpp:24-26): OCP e2m1. */
+float or_fp4_decode(uint8_t nib)
+{
+    static const float lut[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                  -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+    return lut[nib & 15];
+}
+
+int or_floor_log2(float a)
+{
+    uint32_t u = f2u(a) & 0x7FFFFFFFu;
+    int ef = (int)(u >> 23);
+    if (ef > 0)
+        return ef - 127;
+    /* subnormal: value = mant * 2^-149 */
+    uint32_t mant = u & 0x7FFFFFu;
+    int msb = 31 - __builtin_clz(mant);
+    return msb - 149;
+}
+
+/* Mantissa of a in [1, 2) expressed as the 23 fraction bits. */
+static uint32_t frac_bits(float a)
+{
+    uint32_t u = f2u(a) & 0x7FFFFFFFu;
+    if (u >> 23)
+        return u & 0x7FFFFFu;
+    uint32_t mant = u & 0x7FFFFFu;
+    int msb = 31 - __builtin_clz(mant);
+    return (mant << (23 - msb)) & 0x7FFFFFu;
+}
+
+/* 448 = 1.75 * 2^8; 1.75 has fraction bits 0x600000.
+ * floor448: largest e with 448*2^e <= amax.  ceil448: smallest e with
+ * 448*2^e >= amax.  ocp: floor(log2 amax) - 8 (OCP MX v1.0 for E4M3). */
+int or_mx_scale_exp(float amax, int rule)
+{
+    if (!(amax > 0.0f))
+        return -127;
+    if (isinf(amax))
+        return 127;
+    int E = or_floor_log2(amax);
+    uint32_t f = frac_bits(amax);
+    int e;
+    if (rule == 0)
+        e = (f >= 0x600000u) ? E - 8 : E - 9;
+    else if (rule == 1)
+        e = (f <= 0x600000u) ? E - 8 : E - 7;
+    else
+        e = E - 8;
+    if (e < -127)
+        e = -127;
+    if (e > 127)
+        e = 127;
+    return e;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Quantisers                                                                 */
+/* ------------------------------------------------------------------------- */
+void or_quant_mxfp8(const float* x, int rows, int K, uint8_t* q, uint8_t* scales, int rule)
+{
+    int nb = K / 32;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const float* xb = x + (size_t)r * K + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                float a = fabsf(xb[i]);
+                if (a > amax)
+                    amax = a;
+            }
+            int e = or_mx_scale_exp(amax, rule);
+            scales[(size_t)r * nb + b] = (uint8_t)(e + 127);
+            for (int i = 0; i < 32; i++)
+                q[(size_t)r * K + b * 32 + i] = or_e4m3_encode(ldexpf(xb[i], -e));
+        }
+}
+
+/* DeepSeek-style scales: s = amax / 448 in fp32, q = e4m3(x / s); an all-zero
+ * block gets s = 1. */
+static float ds_scale(float amax) { return amax > 0.0f ? amax / 448.0f : 1.0f; }
+
+void or_quant_fp8_1x128(const float* x, int rows, int K, uint8_t* q, float* sfa)
+{
+    int ng = K / 128;
+    for (int r = 0; r < rows; r++)
+        for (int g = 0; g < ng; g++) {
+            const float* xb = x + (size_t)r * K + g * 128;
+            float amax = 0.0f;
+            for (int i = 0; i < 128; i++) {
+                float a = fabsf(xb[i]);
+                if (a > amax)
+                    amax = a;
+            }
+            float s = ds_scale(amax);
+            sfa[(size_t)g * rows + r] = s;
+            for (int i = 0; i < 128; i++)
+                q[(size_t)r * K + g * 128 + i] = or_e4m3_encode(xb[i] / s);
+        }
+}
+
+void or_quant_fp8_128x128(const float* x, int rows, int K, uint8_t* q, float* sfb)
+{
+    int ng = K / 128, nr = (rows + 127) / 128;
+    for (int rb = 0; rb < nr; rb++)
+        for (int g = 0; g < ng; g++) {
+            int r1 = rb * 128 + 128 < rows ? rb * 128 + 128 : rows;
+            float amax = 0.0f;
+            for (int r = rb * 128; r < r1; r++)
+                for (int i = 0; i < 128; i++) {
+                    float a = fabsf(x[(size_t)r * K + g * 128 + i]);
+                    if (a > amax)
+                        amax = a;
+                }
+            float s = ds_scale(amax);
+            sfb[(size_t)rb * ng + g] = s;
+            for (int r = rb * 128; r < r1; r++)
+                for (int i = 0; i < 128; i++)
+                    q[(size_t)r * K + g * 128 + i] =
+                        or_e4m3_encode(x[(size_t)r * K + g * 128 + i] / s);
+        }
+}
+
+void or_quant_fp8_per_tensor(const float* x, size_t n, uint8_t* q, float* scale)
+{
+    float amax = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float a = fabsf(x[i]);
+        if (a > amax)
+            amax = a;
+    }
+    float s = ds_scale(amax);
+    *scale = s;
+    for (size_t i = 0; i < n; i++)
+        q[i] = or_e4m3_encode(x[i] / s);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Layout transforms                                                          */
+/* ------------------------------------------------------------------------- */
+/* shuffle_weight(w, layout=(16,16)), f4gemm_ref.hpp:78-96:
+ *   src.view(N/16, 16, Kp/32, 2, 16).permute(0, 2, 3, 1, 4) */
+void or_shuffle_weight_16x16(const uint8_t* src, uint8_t* dst, int N, int Kp)
+{
+    int nk = Kp / 32;
+    for (int n = 0; n < N; n++)
+        for (int k = 0; k < Kp; k++) {
+            int n0 = n / 16, n1 = n % 16, k0 = k / 32, k1 = (k / 16) % 2, k2 = k % 16;
+            size_t d = ((((size_t)n0 * nk + k0) * 2 + k1) * 16 + n1) * 16 + k2;
+            dst[d] = src[(size_t)n * Kp + k];
+        }
+}
+
+/* shuffle_scale, f4gemm_ref.hpp:98-130:
+ *   pad to [sm, sn] with 0x7F, view(sm/32, 2, 16, sn/8, 2, 4).permute(0, 3, 5, 2, 4, 1) */
+void or_shuffle_scale(const uint8_t* src, uint8_t* dst, int rows, int cols, int sm, int sn)
+{
+    int n3 = sn / 8;
+    for (int r = 0; r < sm; r++)
+        for (int c = 0; c < sn; c++) {
+            uint8_t v = (r < rows && c < cols) ? src[(size_t)r * cols + c] : 0x7F;
+            int d0 = r / 32, d1 = (r / 16) % 2, d2 = r % 16;
+            int d3 = c / 8, d4 = (c / 4) % 2, d5 = c % 4;
+            size_t d = (((((size_t)d0 * n3 + d3) * 4 + d5) * 16 + d2) * 2 + d4) * 2 + d1;
+            dst[d] = v;
+        }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Host launch logic                                                          */
+/* ------------------------------------------------------------------------- */
+/* get_heuristic_kernel as restated by f4gemm.hpp:210-267 (manifest order
+ * breaks ties). */
+int or_select_kernel(int M, int N, int K, int num_cu, int log2_k_split, int bpreshuffle,
+                     const or_cfg* cfgs, int n, int* log2_out)
+{
+    (void)K;
+    uint32_t empty_cu = (uint32_t)num_cu, round = 0xFFFFFFFFu;
+    float effi = 1.0f;
+    int split_en = log2_k_split > 0 ? 1 : 0, bps_en = bpreshuffle ? 1 : 0;
+    int sel = -1, sel_split = 1;
+    for (int i = 0; i < n; i++) {
+        const or_cfg* c = &cfgs[i];
+        if (c->bpreshuffle != bps_en || c->splitK < split_en)
+            continue;
+        if (c->tile_M == 128 && c->tile_N == 512 && (N % c->tile_N) != 0)
+            continue;
+        int list[4], nl;
+        if (log2_k_split >= 0 && c->splitK) {
+            list[0] = 1 << log2_k_split;
+            nl = 1;
+        } else if (c->splitK) {
+            list[0] = 2; list[1] = 4; list[2] = 8; list[3] = 16;
+            nl = 4;
+        } else {
+            list[0] = 1;
+            nl = 1;
+        }
+        for (int j = 0; j < nl; j++) {
+            int tm = (M + c->tile_M - 1) / c->tile_M, tn = (N + c->tile_N - 1) / c->tile_N;
+            uint32_t tg = (uint32_t)(tm * tn * list[j]);
+            uint32_t lr = (tg + num_cu - 1) / num_cu;
+            float le = (float)c->tile_M * c->tile_N / (c->tile_M + c->tile_N);
+            int earlier = lr < round, same = lr == round;
+            int more_busy = empty_cu > (lr * (uint32_t)num_cu - tg);
+            int better = le > effi;
+            if (earlier || (same && (more_busy || better))) {
+                round = lr;
+                empty_cu = lr * (uint32_t)num_cu - tg;
+                effi = le;
+                sel = i;
+                sel_split = list[j];
+            }
+        }
+    }
+    int l2 = 0;
+    while (sel_split >>= 1)
+        ++l2;
+    *log2_out = l2;
+    return sel;
+}
+
+/* make_launch, f4gemm.hpp:329-349. */
+int or_make_launch(const or_cfg* cfg, int M, int N, int K, int log2_k_split, int* gdx,
+                   int* gdy, int* gdz, int* zero_out)
+{
+    *gdz = 1;
+    *zero_out = 0;
+    if (cfg->splitK == 1) {
+        int k_num = 1 << log2_k_split;
+        if (K % k_num != 0)
+            return -1;
+        *zero_out = k_num > 1;
+        int kpt = K / k_num;
+        kpt = ((kpt + 255) / 256) * 256;
+        *gdz = (K + kpt - 1) / kpt;
+    }
+    *gdx = (N + cfg->tile_N - 1) / cfg->tile_N;
+    *gdy = (M + cfg->tile_M - 1) / cfg->tile_M;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* GEMMs                                                                      */
+/* ------------------------------------------------------------------------- */
+void or_reference_gemm(const float* A, const float* B, int M, int N, int K, float alpha,
+                       float* D)
+{
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            double acc = 0.0;
+            const float* a = A + (size_t)m * K;
+            const float* b = B + (size_t)n * K;
+            for (int k = 0; k < K; k++)
+                acc += (double)a[k] * (double)b[k];
+            D[(size_t)m * N + n] = alpha * (float)acc;
+        }
+}
+
+/* Dequantised MX operand in f64: value * 2^(scale-127), exact. */
+static double* mx_dequant(const uint8_t* q, const uint8_t* s, int rows, int K)
+{
+    double* d = (double*)malloc((size_t)rows * K * sizeof(double));
+    for (int r = 0; r < rows; r++)
+        for (int k = 0; k < K; k++) {
+            uint8_t sc = s[(size_t)r * (K / 32) + k / 32];
+            d[(size_t)r * K + k] = (double)or_e4m3_decode(q[(size_t)r * K + k]) *
+                                   (double)or_e8m0_to_f32(sc);
+        }
+    return d;
+}
+
+static double* fp8_dequant(const uint8_t* q, int rows, int K, int ld)
+{
+    double* d = (double*)malloc((size_t)rows * K * sizeof(double));
+    for (int r = 0; r < rows; r++)
+        for (int k = 0; k < K; k++)
+            d[(size_t)r * K + k] = (double)or_e4m3_decode(q[(size_t)r * ld + k]);
+    return d;
+}
+
+/* Sum of exact products over [k0, k1) in extended precision (64-bit
+ * significand): exact whenever the products span fewer than 64 - 8 bits. */
+static long double dot_ld(const double* a, const double* b, int k0, int k1)
+{
+    long double s = 0.0L;
+    for (int k = k0; k < k1; k++)
+        s += (long double)a[k] * (long double)b[k];
+    return s;
+}
+
+void or_gemm_mxfp8_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                         const uint8_t* sB, int M, int N, int K, double* D)
+{
+    double* da = mx_dequant(A, sA, M, K);
+    double* db = mx_dequant(B, sB, N, K);
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            D[(size_t)m * N + n] =
+                (double)dot_ld(da + (size_t)m * K, db + (size_t)n * K, 0, K);
+    free(da);
+    free(db);
+}
+
+void or_gemm_mxfp8_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                           const uint8_t* sB, int M, int N, int K, int log2_k_split,
+                           float alpha, float* D)
+{
+    double* da = mx_dequant(A, sA, M, K);
+    double* db = mx_dequant(B, sB, N, K);
+    int k_num = 1 << log2_k_split;
+    int kpt = ((K / k_num + 255) / 256) * 256;
+    int gdz = (K + kpt - 1) / kpt;
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            const double* a = da + (size_t)m * K;
+            const double* b = db + (size_t)n * K;
+            float total = 0.0f;
+            for (int z = 0; z < gdz; z++) {
+                int kb = z * kpt, ke = kb + kpt < K ? kb + kpt : K;
+                float acc = 0.0f;
+                for (int k = kb; k < ke; k += 128) {
+                    int kend = k + 128 < ke ? k + 128 : ke;
+                    acc = (float)((long double)acc + dot_ld(a, b, k, kend));
+                }
+                total = z == 0 ? acc : total + acc;
+            }
+            D[(size_t)m * N + n] = alpha * total;
+        }
+    free(da);
+    free(db);
+}
+
+static inline float sfb_at(const float* sfb, int g, int n, int stride_sfb, int group_n)
+{
+    return group_n == 1 ? sfb[(size_t)g * stride_sfb + n]
+                        : sfb[(size_t)(n / group_n) * stride_sfb + g];
+}
+
+void or_gemm_blockscale_ref(const uint8_t* A, const uint8_t* B, const float* sfa,
+                            const float* sfb, float* C, int M, int N, int K, int lda,
+                            int ldb, int ldc, int stride_sfa, int stride_sfb, int group_n)
+{
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int g = 0; g < K / 128; g++) {
+                float sa = sfa[(size_t)g * stride_sfa + i];
+                float sb = sfb_at(sfb, g, j, stride_sfb, group_n);
+                float scale = sa * sb;
+                for (int p = g * 128; p < g * 128 + 128; p++) {
+                    float prod = or_e4m3_decode(A[(size_t)i * lda + p]) *
+                                 or_e4m3_decode(B[(size_t)j * ldb + p]);
+                    prod = prod * scale;
+                    sum = sum + prod;
+                }
+            }
+            C[(size_t)i * ldc + j] = sum;
+        }
+}
+
+void or_gemm_blockscale_fp32acc(const uint8_t* A, const uint8_t* B, const float* sfa,
+                                const float* sfb, float* C, int M, int N, int K, int lda,
+                                int ldb, int ldc, int stride_sfa, int stride_sfb,
+                                int group_n)
+{
+    double* da = fp8_dequant(A, M, K, lda);
+    double* db = fp8_dequant(B, N, K, ldb);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float acc = 0.0f;
+            for (int g = 0; g < K / 128; g++) {
+                float p = (float)dot_ld(da + (size_t)i * K, db + (size_t)j * K, g * 128,
+                                        g * 128 + 128);
+                float s = sfa[(size_t)g * stride_sfa + i] * sfb_at(sfb, g, j, stride_sfb, group_n);
+                acc = fmaf(p, s, acc);
+            }
+            C[(size_t)i * ldc + j] = acc;
+        }
+    free(da);
+    free(db);
+}
+
+void or_gemm_blockscale_exact(const uint8_t* A, const uint8_t* B, const float* sfa,
+                              const float* sfb, double* C, int M, int N, int K,
+                              int stride_sfa, int stride_sfb, int group_n)
+{
+    double* da = fp8_dequant(A, M, K, K);
+    double* db = fp8_dequant(B, N, K, K);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            long double acc = 0.0L;
+            for (int g = 0; g < K / 128; g++) {
+                long double p = dot_ld(da + (size_t)i * K, db + (size_t)j * K, g * 128,
+                                       g * 128 + 128);
+                acc += p * (long double)sfa[(size_t)g * stride_sfa + i] *
+                       (long double)sfb_at(sfb, g, j, stride_sfb, group_n);
+            }
+            C[(size_t)i * N + j] = (double)acc;
+        }
+    free(da);
+    free(db);
+}
+
+void or_gemm_per_tensor_fp32acc(const uint8_t* A, const uint8_t* B, float sa, float sb,
+                                float* C, int M, int N, int K)
+{
+    double* da = fp8_dequant(A, M, K, K);
+    double* db = fp8_dequant(B, N, K, K);
+    float s = sa * sb;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k += 128) {
+                int ke = k + 128 < K ? k + 128 : K;
+                acc = (float)((long double)acc +
+                              dot_ld(da + (size_t)i * K, db + (size_t)j * K, k, ke));
+            }
+            C[(size_t)i * N + j] = acc * s;
+        }
+    free(da);
+    free(db);
+}
+
+void or_splitk_reduce(const float* ws, float* out, int split_k, int M, int N, int batch,
+                      int padded_M, int padded_N, const float* bias, int bias_stride_batch)
+{
+    size_t split_stride = (size_t)batch * padded_M * padded_N;
+    for (int b = 0; b < batch; b++)
+        for (int m = 0; m < M; m++)
+            for (int n = 0; n < N; n++) {
+                size_t base = (size_t)b * padded_M * padded_N + (size_t)m * padded_N + n;
+                float acc = ws[base];
+                for (int s = 1; s < split_k; s++)
+                    acc = acc + ws[base + s * split_stride];
+                if (bias)
+                    acc = acc + bias[(size_t)b * bias_stride_batch + n];
+                out[((size_t)b * M + m) * N + n] = acc;
+            }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Synthetic inputs                                                           */
+/* ------------------------------------------------------------------------- */
+static inline uint64_t splitmix64(uint64_t* s)
+{
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static inline double unit_open(uint64_t* s)
+{
+    /* (0, 1): 53 random bits, never 0 */
+    return ((double)(splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+void or_randn(float* out, size_t n, uint64_t seed, float mean, float std)
+{
+    uint64_t s = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        double u1 = unit_open(&s), u2 = unit_open(&s);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + std * r * cos(two_pi * u2));
+        if (i + 1 < n)
+            out[i + 1] = (float)(mean + std * r * sin(two_pi * u2));
+    }
+}
+
+void or_gen_mx_input(float* x, int rows, int K, uint64_t seed, float std, int spread)
+{
+    or_randn(x, (size_t)rows * K, seed, 0.0f, std);
+    uint64_t s = seed ^ 0xA5A5A5A5DEADBEEFull;
+    int nb = K / 32;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            int u = spread > 0 ? (int)(splitmix64(&s) % (uint64_t)(2 * spread + 1)) - spread : 0;
+            for (int i = 0; i < 32; i++)
+                x[(size_t)r * K + b * 32 + i] = ldexpf(x[(size_t)r * K + b * 32 + i], u);
+        }
+}

@@ -1,0 +1,186 @@
+"""GPU parity of the MXFP8 GEMM (f4gemm ABI) against the CPU oracle.
+
+Cases follow the reference's regression sweep (asm_f4gemm/run_tests.sh:37-57):
+a heuristic shape sweep, every manifest kernel at M=300 N=2048 K=1024, and
+split-K with log2 splits 1..4; plus config 1 of the benchmark, decode shapes,
+alpha/beta and error paths. Expected values come from
+oracle.gemm_mxfp8_fp32acc (exact 128-K step sums accumulated in fp32 in the
+kernel's K order, slices summed in order) rounded to bf16; the tolerance is
+the north-star rule in helpers.bf16_compare, with the MFMA truncation bound
+(helpers.MFMA_BOUND_FACTOR) for outputs that cancel.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gcnasm_amd import _lib, f4gemm
+from gcnasm_amd._lib import GaError
+from helpers import bf16_compare, mx_operands
+
+pytestmark = pytest.mark.gpu
+
+
+def run_mx(dev, qa, sa, qb, sb, cfg, log2_k_split=0, alpha=1.0, beta=0.0, c_in=None,
+           workspace=None):
+    M, K = qa.shape
+    N = qb.shape[0]
+    sh = f4gemm.Shape(M, N, K)
+    a_pad = np.zeros((sh.a_rows_pad(), K), dtype=np.uint8)
+    a_pad[:M] = qa
+    A = torch.from_numpy(a_pad).to(dev)
+    bh = f4gemm.shuffle_weight_16x16(qb, N, K) if cfg.bpreshuffle else qb.reshape(-1)
+    B = torch.from_numpy(np.ascontiguousarray(bh)).to(dev)
+    SA = torch.from_numpy(f4gemm.shuffle_scale(sa, M, K // 32, sh.scale_a_rows(),
+                                               sh.scale_cols())).to(dev)
+    SB = torch.from_numpy(f4gemm.shuffle_scale(sb, N, K // 32, sh.scale_b_rows(),
+                                               sh.scale_cols())).to(dev)
+    D = torch.full((sh.d_rows_pad(), N), float("nan"), dtype=torch.bfloat16, device=dev)
+    C = None
+    if c_in is not None:
+        C = torch.from_numpy(c_in.view(np.int16)).to(dev).view(torch.bfloat16)
+    ld = f4gemm.make_launch(cfg, M, N, K, log2_k_split)
+    args = f4gemm.fill_args(D, C, A, B, SA, SB, M, N, K, N, sh.scale_cols(), sh.scale_cols(),
+                            alpha, beta, ld.log2_k_split)
+    k = f4gemm.Kernel().load(None, cfg)
+    k.launch(args, ld.gdx, ld.gdy, ld.gdz, workspace=workspace)
+    torch.cuda.synchronize()
+    out = D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+    return out, ld
+
+
+def expect(qa, sa, qb, sb, log2_k_split=0, alpha=1.0):
+    return oracle.to_bf16_bits(oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, log2_k_split, alpha))
+
+
+def check(got, want, label, absdot):
+    ok, st = bf16_compare(got, want, absdot)
+    print("%s: exact=%.5f max_ulp=%d bounded=%d bad=%d/%d" % (
+        label, st["exact"], st["max_ulp"], st["bounded"], st["bad"], st["n"]), flush=True)
+    assert st["bad"] == 0, "%s: %d outputs outside tolerance" % (label, st["bad"])
+    return st
+
+
+def cfg_named(name):
+    for c in f4gemm.manifest():
+        if c.knl_name == name:
+            return c
+    raise KeyError(name)
+
+
+def test_config1_heuristic(dev):
+    """Benchmark config 1: M=256 N=256 K=512 through the heuristic choice."""
+    M, N, K = 256, 256, 512
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=1)
+    idx, l2 = f4gemm.select_kernel(M, N, K, 256, 0, 1)
+    cfg = f4gemm.manifest()[idx]
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    st = check(got, expect(qa, sa, qb, sb, l2), "config1 " + cfg.knl_name,
+               oracle.mx_absdot(qa, sa, qb, sb))
+    # all but the MFMA-truncation residue is bit-identical to the oracle
+    assert st["exact"] > 0.98
+
+
+@pytest.mark.parametrize("shape", [(128, 1024, 1024), (256, 2048, 2048), (300, 2048, 1024),
+                                   (1, 4096, 2048), (17, 512, 256), (512, 1024, 2048),
+                                   (2048, 8192, 1024), (4096, 4096, 512)])
+def test_heuristic_sweep(dev, shape):
+    M, N, K = shape
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M + N + K)
+    idx, l2 = f4gemm.select_kernel(M, N, K, 256, 0, 1)
+    cfg = f4gemm.manifest()[idx]
+    rows = slice(None) if M * N * K <= 2 ** 32 else slice(0, 256)
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    want = expect(qa[rows], sa[rows], qb, sb, l2)
+    check(got[rows], want, "sweep %s %s" % (shape, cfg.knl_name),
+          oracle.mx_absdot(qa[rows], sa[rows], qb, sb))
+
+
+@pytest.mark.parametrize("name", [c.knl_name for c in f4gemm.manifest()])
+def test_every_kernel(dev, name):
+    M, N, K = 300, 2048, 1024
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=3)
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0)
+    check(got, expect(qa, sa, qb, sb, 0), name, oracle.mx_absdot(qa, sa, qb, sb))
+
+
+@pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x128_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_32x256_splitK"])
+@pytest.mark.parametrize("l2", [1, 2, 3, 4])
+def test_splitk(dev, name, l2):
+    M, N, K = 256, 1024, 4096
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=10 + l2)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    assert ld.gdz == 1 << l2
+    check(got, expect(qa, sa, qb, sb, l2), "%s splitk=%d" % (name, l2),
+          oracle.mx_absdot(qa, sa, qb, sb))
+
+
+@pytest.mark.parametrize("M", [1, 16, 64])
+@pytest.mark.parametrize("NK", [(2048, 4096), (1024, 8192)])
+def test_decode_shapes(dev, M, NK):
+    """Decode-shaped GEMMs (weights from N(0, 0.02)) with the heuristic's split-K."""
+    N, K = NK
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M, std_b=0.02)
+    idx, l2 = f4gemm.select_kernel(M, N, K, 256, -1, 1)
+    cfg = f4gemm.manifest()[idx]
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    check(got, expect(qa, sa, qb, sb, l2), "decode M=%d N=%d K=%d %s gdz=%d" %
+          (M, N, K, cfg.knl_name, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
+def test_alpha_beta(dev):
+    M, N, K = 128, 256, 512
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=77)
+    rng = np.random.default_rng(5)
+    c = oracle.to_bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_128x128")
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0, alpha=0.5, beta=2.0, c_in=c)
+    acc = oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, 0, 1.0)
+    v = (np.float32(0.5) * acc).astype(np.float32)
+    v = (v + (np.float32(2.0) * oracle.bf16_bits_to_f32(c)).astype(np.float32)).astype(np.float32)
+    check(got, oracle.to_bf16_bits(v), "alpha/beta", 0.5 * oracle.mx_absdot(qa, sa, qb, sb))
+
+
+def test_explicit_workspace_and_too_small(dev):
+    M, N, K = 64, 512, 2048
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=9)
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_64x256_splitK")
+    ws = torch.empty(4 * M * N, dtype=torch.float32, device=dev)
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 2, workspace=ws)
+    check(got, expect(qa, sa, qb, sb, 2), "explicit workspace", oracle.mx_absdot(qa, sa, qb, sb))
+    small = torch.empty(16, dtype=torch.float32, device=dev)
+    with pytest.raises(GaError) as e:
+        run_mx(dev, qa, sa, qb, sb, cfg, 2, workspace=small)
+    assert e.value.status == _lib.GA_ERR_WORKSPACE
+
+
+def test_rejects_bad_shapes(dev):
+    l = _lib.lib()
+    args = _lib.F4gemmKargs()
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    l.ga_fill_args(ctypes.byref(args), buf.data_ptr(), None, buf.data_ptr(), buf.data_ptr(),
+                   buf.data_ptr(), buf.data_ptr(), 64, 64, 200, 64, 8, 8, 1.0, 0.0, 0)
+    st = l.ga_kernel_launch(0, ctypes.byref(args), 1, 1, 1, None, 0, None)
+    assert st == _lib.GA_ERR_SHAPE  # K % 128
+
+
+def test_one_call_mxfp8_gemm_from_float(dev):
+    """ga_mxfp8_gemm over operands prepared on the GPU (quantiser + shuffles)."""
+    from gcnasm_amd import ops
+    M, N, K = 192, 768, 1024
+    xa = oracle.gen_mx_input(M, K, 42, 1.0, 4)
+    xb = oracle.gen_mx_input(N, K, 43, 1.0, 4)
+    a = ops.prepare_mx_a(torch.from_numpy(xa).to(dev))
+    b = ops.prepare_mx_b(torch.from_numpy(xb).to(dev))
+    D, idx, ld = ops.mxfp8_gemm(a, b)
+    torch.cuda.synchronize()
+    qa, sa = oracle.quant_mxfp8(xa)
+    qb, sb = oracle.quant_mxfp8(xb)
+    got = D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+    check(got, expect(qa, sa, qb, sb, ld.log2_k_split), "one-call",
+          oracle.mx_absdot(qa, sa, qb, sb))

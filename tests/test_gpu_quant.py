@@ -1,0 +1,102 @@
+"""GPU quantisers and device shuffles: bit-exact against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gcnasm_amd import f4gemm, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def edge_values():
+    """Ties, subnormal boundaries, saturation, zeros of both signs, inf/NaN."""
+    vals = [0.0, -0.0, 448.0, -448.0, 464.0, 480.0, 1e30, -1e30, np.inf, -np.inf,
+            2.0 ** -6, 2.0 ** -7, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -10, 1.0625, 1.1875,
+            1.0 + 2.0 ** -4, 1.0 + 3 * 2.0 ** -4, 3.0e-45]
+    # midpoints between consecutive E4M3 values (exact ties)
+    t = oracle.e4m3_decode_table()
+    pos = np.sort(t[np.isfinite(t) & (t > 0)])
+    mids = (pos[:-1] + pos[1:]) / 2
+    return np.concatenate([np.array(vals, dtype=np.float32), mids.astype(np.float32),
+                           -mids.astype(np.float32)])
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+@pytest.mark.parametrize("in_bf16", [False, True])
+def test_quant_mx(dev, rule, in_bf16):
+    rows, K = 96, 1024
+    x = oracle.gen_mx_input(rows, K, 100 + rule, 1.0, 6)
+    e = edge_values()
+    x.reshape(-1)[: e.size] = e
+    if in_bf16:
+        xb = oracle.to_bf16_bits(x)
+        x = oracle.bf16_bits_to_f32(xb)
+        xt = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x).to(dev)
+    q, s = ops.quant_mxfp8(xt, rule)
+    torch.cuda.synchronize()
+    qo, so = oracle.quant_mxfp8(x, rule)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+
+
+@pytest.mark.parametrize("in_bf16", [False, True])
+def test_quant_1x128_128x128_per_tensor(dev, in_bf16):
+    rows, K = 300, 1024
+    x = oracle.randn(rows * K, 7).reshape(rows, K) * np.float32(3.0)
+    x[5, :128] = 0.0  # an all-zero group
+    x.reshape(-1)[1000:1000 + 40] = edge_values()[:40]
+    x[np.isinf(x)] = 1000.0
+    if in_bf16:
+        xb = oracle.to_bf16_bits(x)
+        x = oracle.bf16_bits_to_f32(xb)
+        xt = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    q1, s1 = ops.quant_fp8_1x128(xt)
+    q2, s2 = ops.quant_fp8_128x128(xt)
+    q3, s3 = ops.quant_fp8_per_tensor(xt)
+    torch.cuda.synchronize()
+    o1, os1 = oracle.quant_fp8_1x128(x)
+    o2, os2 = oracle.quant_fp8_128x128(x)
+    o3, os3 = oracle.quant_fp8_per_tensor(x)
+    np.testing.assert_array_equal(s1.cpu().numpy().view(np.uint32), os1.view(np.uint32))
+    np.testing.assert_array_equal(q1.cpu().numpy(), o1)
+    np.testing.assert_array_equal(s2.cpu().numpy().view(np.uint32), os2.view(np.uint32))
+    np.testing.assert_array_equal(q2.cpu().numpy(), o2)
+    np.testing.assert_array_equal(s3.cpu().numpy().view(np.uint32), os3.view(np.uint32))
+    np.testing.assert_array_equal(q3.cpu().numpy(), o3)
+
+
+@pytest.mark.parametrize("NK", [(16, 32), (256, 512), (272, 4096)])
+def test_device_shuffle_weight(dev, NK):
+    N, Kp = NK
+    rng = np.random.default_rng(N + Kp)
+    w = rng.integers(0, 256, size=(N, Kp), dtype=np.uint8)
+    got = ops.shuffle_weight_16x16(torch.from_numpy(w).to(dev)).cpu().numpy().reshape(-1)
+    np.testing.assert_array_equal(got, oracle.shuffle_weight_16x16(w, N, Kp))
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 256, 8), (300, 32, 512, 32), (17, 5, 32, 8)])
+def test_device_shuffle_scale(dev, shape):
+    rows, cols, sm, sn = shape
+    rng = np.random.default_rng(rows)
+    s = rng.integers(100, 140, size=(rows, cols), dtype=np.uint8)
+    got = ops.shuffle_scale(torch.from_numpy(s).to(dev), sm, sn).cpu().numpy()
+    np.testing.assert_array_equal(got, oracle.shuffle_scale(s, rows, cols, sm, sn))
+
+
+def test_prepare_matches_host_path(dev):
+    """prepare_mx_b on the GPU == oracle quantiser + host shuffles."""
+    N, K = 256, 768
+    x = oracle.gen_mx_input(N, K, 5, 0.02, 4)
+    b = ops.prepare_mx_b(torch.from_numpy(x).to(dev))
+    q, s = oracle.quant_mxfp8(x)
+    sh = f4gemm.Shape(1, N, K)
+    np.testing.assert_array_equal(b.codes.cpu().numpy().reshape(-1),
+                                  oracle.shuffle_weight_16x16(q, N, K))
+    np.testing.assert_array_equal(b.scales.cpu().numpy(),
+                                  oracle.shuffle_scale(s, N, K // 32, sh.scale_b_rows(),
+                                                       sh.scale_cols()))
