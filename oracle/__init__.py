@@ -16,6 +16,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libgcnasm_ref.so")
+HIPFP8_LIB = os.path.join(HERE, "libhipfp8.so")
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -28,6 +29,7 @@ _u64 = ctypes.c_uint64
 _SIGS = {
     "or_e4m3_encode": (_u8, [_f]),
     "or_e4m3_decode": (_f, [_u8]),
+    "or_e4m3_encode_n": (None, [_vp, _vp, _sz]),
     "or_e8m0_to_f32": (_f, [_u8]),
     "or_f32_to_bf16": (_u16, [_f]),
     "or_bf16_to_f32": (_f, [_u16]),
@@ -106,6 +108,17 @@ def load_ref():
     return _R
 
 
+def hipfp8_encode(x):
+    """ROCm's host __hip_fp8_e4m3 conversion of float32 values (None if not built)."""
+    if not os.path.exists(HIPFP8_LIB):
+        return None
+    lib = ctypes.CDLL(HIPFP8_LIB)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib.hipfp8_encode_e4m3(p(x), p(out), ctypes.c_long(x.size))
+    return out
+
+
 def p(a):
     """ctypes pointer of a C-contiguous numpy array."""
     assert a.flags["C_CONTIGUOUS"]
@@ -172,6 +185,13 @@ def shuffle_scale(src, rows, cols, sm, sn):
     dst = np.empty(sm * sn, dtype=np.uint8)
     load().or_shuffle_scale(p(src), p(dst), rows, cols, sm, sn)
     return dst
+
+
+def e4m3_encode(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    load().or_e4m3_encode_n(p(x), p(out), x.size)
+    return out
 
 
 def e4m3_decode_table():

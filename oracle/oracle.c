@@ -80,6 +80,12 @@ uint8_t or_e4m3_encode(float x)
     return sign | (uint8_t)code;
 }
 
+void or_e4m3_encode_n(const float* x, uint8_t* out, size_t n)
+{
+    for (size_t i = 0; i < n; i++)
+        out[i] = or_e4m3_encode(x[i]);
+}
+
 /* f4gemm_ref.hpp:29-41: value 2^(e-127); e == 0 -> bits 0x00400000; 0xFF -> NaN. */
 float or_e8m0_to_f32(uint8_t e)
 {

@@ -21,6 +21,7 @@ extern "C" {
 
 /* ---- scalar codecs ------------------------------------------------------ */
 uint8_t or_e4m3_encode(float x);      /* OCP E4M3, RNE, saturate to +-448, NaN->0x7F */
+void or_e4m3_encode_n(const float* x, uint8_t* out, size_t n);
 float or_e4m3_decode(uint8_t c);      /* opus.hpp:858-871 value set (OCP, bias 7)      */
 float or_e8m0_to_f32(uint8_t e);      /* f4gemm_ref.hpp:29-41                          */
 uint16_t or_f32_to_bf16(float x);     /* RNE, opus.hpp:944-950                         */

@@ -1,0 +1,82 @@
+"""The C ABI library (CPU only, no compute on a GPU): it loads, exports every
+entry point declared in include/gcnasm_amd.h, its structs have the reference's
+byte layout, and argument errors come back as status codes (validated before
+any HIP call, so these run without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from gcnasm_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "gcnasm_amd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ga_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared_functions()
+    assert len(names) >= 25
+    l = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in names if not hasattr(l, n)]
+    assert not missing, missing
+    # and the Python binding covers all of them
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_struct_sizes():
+    assert ctypes.sizeof(_lib.OpusGemmKargs) == 96
+    assert ctypes.sizeof(_lib.F4gemmKargs) == 0x174
+    assert ctypes.sizeof(_lib.TileConfig) == 16 + 2 * _lib.GA_NAME_MAX
+
+
+def test_status_strings():
+    l = _lib.lib()
+    for s in range(10):
+        assert l.ga_status_string(s)
+    assert b"gfx950" in l.ga_version()
+
+
+def test_null_arguments_are_rejected_before_any_device_call():
+    l = _lib.lib()
+    assert l.ga_kernel_launch(0, None, 1, 1, 1, None, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_kernel_launch(-1, None, 1, 1, 1, None, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_gemm_a8w8_blockscale(None, 128, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_fp8_gemm_per_tensor(None, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_quant_mxfp8(None, 0, 1, 32, 32, None, 32, None, 1, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_quant_fp8_1x128(None, 0, 1, 128, 128, None, 128, None, 1, None) == _lib.GA_ERR_ARG
+    assert l.ga_quant_fp8_128x128(None, 0, 1, 128, 128, None, 128, None, 1, None) == _lib.GA_ERR_ARG
+    assert l.ga_quant_fp8_per_tensor(None, 0, 4, None, None, None, None) == _lib.GA_ERR_ARG
+    assert l.ga_splitk_reduce(None, None, 0, 1, 1, 1, 1, 1, 1, None, 0, 0, None) == _lib.GA_ERR_ARG
+    assert l.ga_shuffle_weight_16x16_device(None, None, 16, 32, None) == _lib.GA_ERR_ARG
+    assert l.ga_shuffle_scale_device(None, None, 1, 1, 32, 8, None) == _lib.GA_ERR_ARG
+    assert l.ga_manifest_get(10 ** 6, None) == _lib.GA_ERR_ARG
+    assert b"range" in l.ga_last_error()
+
+
+def test_opus_kargs_validation():
+    l = _lib.lib()
+    ka = _lib.OpusGemmKargs()
+    ka.ptr_a = ka.ptr_b = ka.ptr_c = ka.ptr_sfa = ka.ptr_sfb = 0x1000
+    ka.m, ka.n, ka.k, ka.batch = 64, 64, 200, 1  # K % 128 != 0
+    ka.stride_a = ka.stride_b = 208
+    ka.stride_c = 64
+    assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 128, 0, None) == _lib.GA_ERR_GROUP
+    ka.k = 0
+    assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 128, 0, None) == _lib.GA_ERR_ARG
+    ka.k = ka.stride_a = ka.stride_b = 256
+    assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 64, 0, None) == _lib.GA_ERR_ARG
+
+
+def test_mx_launch_validation_without_gpu():
+    l = _lib.lib()
+    args = _lib.F4gemmKargs()
+    l.ga_fill_args(ctypes.byref(args), 8, None, 8, 8, 8, 8, 64, 64, 256, 64, 8, 8, 1.0, 0.0, 0)
+    assert l.ga_kernel_launch(0, ctypes.byref(args), 99, 1, 1, None, 0, None) == _lib.GA_ERR_ARG
+    l.ga_fill_args(ctypes.byref(args), 8, None, 8, 8, 8, 8, 64, 60, 256, 64, 8, 8, 1.0, 0.0, 0)
+    assert l.ga_kernel_launch(0, ctypes.byref(args), 1, 1, 1, None, 0, None) == _lib.GA_ERR_SHAPE
