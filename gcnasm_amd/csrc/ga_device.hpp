@@ -78,6 +78,16 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Workgroup barrier for LDS handoff without a memory-model fence: the fence
+// of __syncthreads() also drains every outstanding direct-to-LDS load
+// (vmcnt(0)), which would serialise a multi-stage pipeline. Callers wait for
+// the loads they need with wait_vmcnt<N>() first; the "memory" clobber keeps
+// the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void barrier_lds()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ void wait_lgkmcnt0()
 {
     __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4) | (0x0 << 8));

@@ -29,7 +29,8 @@ struct MxKernel {
     ga_tile_config cfg;
     mx_launch_fn launch;
 };
-int mx_registry_count();
+int mx_registry_count();  // manifest rows
+int mx_registry_total();  // manifest rows + kernels reachable only by name
 const MxKernel* mx_registry_get(int idx);
 
 // Library-owned per-device fp32 workspace, grown on demand.

@@ -37,25 +37,35 @@
 
 namespace ga {
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, bool BPS_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, bool BPS_, int NS_ = 2>
 struct MxCfg {
     static constexpr int BM = BM_, BN = BN_;
     static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
     static constexpr bool BPS = BPS_;
+    static constexpr int NS = NS_; // LDS stages in flight
     static constexpr int NT = 256;
     static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     static constexpr int TM = WTM / 16, TN = WTN / 16;
+    static constexpr int SM = TM / 2, SN = TN / 2; // scale dwords: one per 32 rows
     static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS = 2 * STAGE;
+    // E8M0 scales travel with each stage: one 256-byte shuffled block per 32
+    // rows of A and of B (all 4 x 16 MFMA lanes' dwords), copied by the waves
+    // in turn (padded to a multiple of 4 with repeats of block 0).
+    static constexpr int SBLK = BM / 32 + BN / 32;
+    static constexpr int S_LOADS = (SBLK + 3) / 4; // per wave per stage
+    static constexpr int S_BYTES = 4 * S_LOADS * 256;
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int LDS = NS * STAGE;
     static constexpr int A_LOADS = A_BYTES / (NT * 16);
     static constexpr int B_LOADS = B_BYTES / (NT * 16);
+    static constexpr int TILE_LOADS = A_LOADS + B_LOADS + S_LOADS; // vmem ops per stage
     static_assert(WAVES_M * WAVES_N == 4, "4 waves");
     // 32-aligned wave tiles: the row half of each 16-row MFMA tile inside a
     // 32-row scale block is (tile index & 1), known at compile time.
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile multiple of 32");
     static_assert(A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "tile >= 32 rows");
     static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NS >= 2 && TILE_LOADS * (NS - 2) < 64, "vmcnt range");
 };
 
 constexpr int kGroupM = 4; // M-tiles per L2 group
@@ -83,17 +93,21 @@ struct MxState {
     __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
     uint32_t voff_a[C::A_LOADS];
     uint32_t voff_b[C::B_LOADS];
-    uint32_t soff_a[C::TM]; // scale dword byte offset of each A row tile (group 0)
-    uint32_t soff_b[C::TN];
-    uint32_t b_kstride; // bytes per K step of 128 in B
+    uint32_t soff[C::S_LOADS]; // scale dword offset of this wave's blocks (first K group)
+    bool sfrom_b[C::S_LOADS];  // block is a B block (else A)
+    uint32_t b_kstride;        // bytes per K step of 128 in B
 };
 
+// Direct-to-LDS copy of 128-K step `step` of the slice (global K offset kk)
+// into stage `buf`: A and B tiles, then this wave's scale blocks. The scale
+// dword covers 256 K (bytes 2*d4 + d1, d4 = step & 1, d1 = 16-row half).
 template <class C>
-__device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, int buf, int kk,
-                                            int wave)
+__device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, int buf, int step,
+                                            int kk, int wave)
 {
     char* sa = smem + buf * C::STAGE;
     char* sb = sa + C::A_BYTES;
+    char* ss = sb + C::B_BYTES;
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; i++)
         lds_load16(st.ra, (lds_void*)(sa + (i * 256 + wave * 64) * 16), st.voff_a[i] + kk, 0);
@@ -101,30 +115,34 @@ __device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, in
     for (int i = 0; i < C::B_LOADS; i++)
         lds_load16(st.rb, (lds_void*)(sb + (i * 256 + wave * 64) * 16),
                    st.voff_b[i] + (uint32_t)(kk / 128) * st.b_kstride, 0);
+    const uint32_t q = (uint32_t)(step >> 1) * 256;
+#pragma unroll
+    for (int i = 0; i < C::S_LOADS; i++) {
+        lds_void* dst = (lds_void*)(ss + (wave * C::S_LOADS + i) * 256);
+        if (st.sfrom_b[i])
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(st.rsb, dst, 4, st.soff[i] + q, 0, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(st.rsa, dst, 4, st.soff[i] + q, 0, 0, 0);
+    }
 }
 
 template <class C>
-__device__ __forceinline__ void load_scales(const MxState<C>& st, int q, uint32_t (&sa)[C::TM],
-                                            uint32_t (&sb)[C::TN])
-{
-    // q-th group of 256 K; consecutive groups are 256 bytes apart.
-#pragma unroll
-    for (int t = 0; t < C::TM; t++)
-        sa[t] = buf_load4(st.rsa, st.soff_a[t] + q * 256, 0);
-#pragma unroll
-    for (int t = 0; t < C::TN; t++)
-        sb[t] = buf_load4(st.rsb, st.soff_b[t] + q * 256, 0);
-}
-
-template <class C, int PAR>
-__device__ __forceinline__ void compute_stage(const char* smem, int buf, int wm, int wn, int lane,
-                                              const uint32_t (&sa)[C::TM],
-                                              const uint32_t (&sb)[C::TN],
-                                              v4f (&acc)[C::TM][C::TN])
+__device__ __forceinline__ void compute_stage(const char* smem, int buf, int step, int wm, int wn,
+                                              int lane, v4f (&acc)[C::TM][C::TN])
 {
     const char* la = smem + buf * C::STAGE;
     const char* lb = la + C::A_BYTES;
+    const char* ls = lb + C::B_BYTES;
     const int lo = lane * 16;
+    // this step's 128-K half of each scale dword moved to bytes 0-1
+    const uint32_t sh = (uint32_t)(step & 1) * 16;
+    uint32_t sa[C::SM], sb[C::SN];
+#pragma unroll
+    for (int t = 0; t < C::SM; t++)
+        sa[t] = *(const uint32_t*)(ls + (wm * C::SM + t) * 256 + lane * 4) >> sh;
+#pragma unroll
+    for (int t = 0; t < C::SN; t++)
+        sb[t] = *(const uint32_t*)(ls + (C::BM / 32 + wn * C::SN + t) * 256 + lane * 4) >> sh;
     v8i bf[C::TN];
 #pragma unroll
     for (int t = 0; t < C::TN; t++) {
@@ -141,9 +159,10 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int wm,
         v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
         static_for<C::TN>([&](auto T) {
             constexpr int t = decltype(T)::value;
-            // op_sel picks byte (128-K half, 16-row half) of the scale dword
-            acc[i][t] = mfma_mx16<PAR * 2 + (t & 1), PAR * 2 + (i & 1)>(bf[t], af, acc[i][t],
-                                                                      (int)sb[t], (int)sa[i]);
+            // op_sel picks the 16-row half inside the 32-row scale block; the
+            // 128-K half was selected by the caller's shift of the dword
+            acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(bf[t], af, acc[i][t], (int)sb[t >> 1],
+                                                    (int)sa[i >> 1]);
         });
     });
 }
@@ -183,7 +202,7 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
             int idx = i * 256 + tid;
             int g = idx >> 7, u = idx & 127;
             int row = g * 16 + (u & 15);
-            st.voff_a[i] = (uint32_t)row * lda + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+            st.voff_a[i] = (uint32_t)row * lda + (u >> 4) * 16;
         }
         if (C::BPS) {
             const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
@@ -206,7 +225,7 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
                 int idx = i * 256 + tid;
                 int g = idx >> 7, u = idx & 127;
                 int row = g * 16 + (u & 15);
-                st.voff_b[i] = (uint32_t)row * ldb + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
+                st.voff_b[i] = (uint32_t)row * ldb + (u >> 4) * 16;
             }
         }
         // Scales: shuffled layout, 256-byte block per (32 rows, 256 K).
@@ -215,14 +234,14 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         st.rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)smb * snb);
         const int q0 = kb / 256;
 #pragma unroll
-        for (int t = 0; t < C::TM; t++) {
-            int r = m0 + wm * C::WTM + t * 16;
-            st.soff_a[t] = ((uint32_t)(r / 32) * (sna / 8) + q0) * 256 + lane * 4;
-        }
-#pragma unroll
-        for (int t = 0; t < C::TN; t++) {
-            int r = n0 + wn * C::WTN + t * 16;
-            st.soff_b[t] = ((uint32_t)(r / 32) * (snb / 8) + q0) * 256 + lane * 4;
+        for (int i = 0; i < C::S_LOADS; i++) {
+            int j = wave * C::S_LOADS + i;
+            j = j < C::SBLK ? j : 0; // padding slots repeat block 0
+            const bool isb = j >= C::BM / 32;
+            const int r = isb ? n0 + (j - C::BM / 32) * 32 : m0 + j * 32;
+            const uint32_t sn = isb ? snb : sna;
+            st.sfrom_b[i] = isb;
+            st.soff[i] = ((uint32_t)(r / 32) * (sn / 8) + q0) * 256 + lane * 4;
         }
     }
 
@@ -233,44 +252,27 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         for (int t = 0; t < C::TN; t++)
             acc[i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    // K loop: pairs of 128-K steps (one 256-K scale group per pair, stage 0
-    // then stage 1), then an optional single tail step in stage 0.
-    uint32_t sa[C::TM], sb[C::TN], na[C::TM], nb[C::TN];
-    const int npairs = nsteps >> 1;
-    if (nsteps > 0) {
-        issue_stage<C>(st, smem, 0, kb, wave);
-        load_scales<C>(st, 0, sa, sb);
-    }
-    for (int p = 0; p < npairs; p++) {
-        const int s = 2 * p;
-        wait_vmcnt<0>();
-        __syncthreads();
-        issue_stage<C>(st, smem, 1, kb + (s + 1) * 128, wave);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_stage<C, 0>(smem, 0, wm, wn, lane, sa, sb, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<0>();
-        __syncthreads();
-        // Issued unconditionally to keep the loop body branch-free: on the
-        // last pair this prefetches the tail step, or re-reads in-bounds
-        // bytes past the slice (never used), and range-checked loads past
-        // the end of A, B or a scale buffer return zero.
-        issue_stage<C>(st, smem, 0, kb + (s + 2) * 128, wave);
-        load_scales<C>(st, p + 1, na, nb);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_stage<C, 1>(smem, 1, wm, wn, lane, sa, sb, acc);
-        __builtin_amdgcn_sched_barrier(0);
+    // Pipeline: stages 0 .. NS-2 in flight before the loop; step s waits for
+    // its stage (counted vmcnt; every load of the loop is a direct-to-LDS copy,
+    // so no other wait is generated), then issues stage s+NS-1 into the buffer
+    // step s-1 used (free after the barrier) and computes from stage s. Loads
+    // past the slice are issued unconditionally (branch-free body): they read
+    // in-bounds bytes that are never used, or range-checked zeros past the end
+    // of a buffer.
 #pragma unroll
-        for (int t = 0; t < C::TM; t++)
-            sa[t] = na[t];
-#pragma unroll
-        for (int t = 0; t < C::TN; t++)
-            sb[t] = nb[t];
-    }
-    if (nsteps & 1) {
-        wait_vmcnt<0>();
-        __syncthreads();
-        compute_stage<C, 0>(smem, 0, wm, wn, lane, sa, sb, acc);
+    for (int p = 0; p < C::NS - 1; p++)
+        issue_stage<C>(st, smem, p, p, kb + p * 128, wave);
+    int buf = 0;
+    for (int s = 0; s < nsteps; s++) {
+        wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
+        barrier_lds();
+        int nbuf = buf + C::NS - 1;
+        nbuf = nbuf >= C::NS ? nbuf - C::NS : nbuf;
+        issue_stage<C>(st, smem, nbuf, s + C::NS - 1, kb + (s + C::NS - 1) * 128, wave);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_stage<C>(smem, buf, s, wm, wn, lane, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        buf = buf + 1 == C::NS ? 0 : buf + 1;
     }
 
     // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile. The library is
@@ -316,32 +318,39 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
     hipLaunchKernelGGL(mx_gemm_kernel<C>, dim3(gdx, gdy, gdz), dim3(256), 0, stream, args, ws);
 }
 
-#define GA_MX_ENTRY(BM, BN, WGM, WGN, BPS, SPLIT, SUFFIX)                                      \
+#define GA_MX_ENTRY(BM, BN, WGM, WGN, BPS, NS, SPLIT, SUFFIX)                                  \
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0)>>}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
-// Manifest order matters: the heuristic breaks ties by it.
+// Manifest order matters: the heuristic breaks ties by it. Entries after
+// kManifestCount are found by name (ga_kernel_find) but are not offered to the
+// heuristic.
 static const MxKernel g_mx_kernels[] = {
-    GA_MX_ENTRY(256, 128, 2, 2, 1, 0, ""),
-    GA_MX_ENTRY(128, 256, 2, 2, 1, 0, ""),
-    GA_MX_ENTRY(128, 128, 2, 2, 1, 0, ""),
-    GA_MX_ENTRY(64, 256, 1, 4, 1, 0, ""),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 0, ""),
-    GA_MX_ENTRY(256, 128, 2, 2, 1, 1, "_splitK"),
-    GA_MX_ENTRY(128, 256, 2, 2, 1, 1, "_splitK"),
-    GA_MX_ENTRY(128, 128, 2, 2, 1, 1, "_splitK"),
-    GA_MX_ENTRY(64, 256, 1, 4, 1, 1, "_splitK"),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 1, "_splitK"),
-    GA_MX_ENTRY(32, 512, 1, 4, 1, 1, "_splitK"),
-    GA_MX_ENTRY(256, 128, 2, 2, 0, 0, ""),
-    GA_MX_ENTRY(128, 128, 2, 2, 0, 1, "_splitK"),
+    GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
+    GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 0, ""),
+    GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 0, ""),
+    GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
+    GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 1, "_splitK"),
+    GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 1, "_splitK"),
+    GA_MX_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
+    GA_MX_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
+    GA_MX_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
+    // not in the manifest
+    GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
+    GA_MX_ENTRY(256, 128, 2, 2, 1, 2, 0, "_ns2"),
 };
+constexpr int kManifestCount = 13;
 
-int mx_registry_count() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
+int mx_registry_count() { return kManifestCount; }
+int mx_registry_total() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
 const MxKernel* mx_registry_get(int idx) { return &g_mx_kernels[idx]; }
 
 ga_status default_workspace(size_t bytes, void** ptr)
@@ -378,7 +387,7 @@ ga_status ga_kernel_find(const char* name, int* idx)
 {
     if (!name || !idx)
         return fail(GA_ERR_ARG, "null argument");
-    for (int i = 0; i < mx_registry_count(); i++) {
+    for (int i = 0; i < mx_registry_total(); i++) {
         const ga_tile_config& c = g_mx_kernels[i].cfg;
         if (!strcmp(c.knl_name, name) || !strcmp(c.co_name, name)) {
             *idx = i;
@@ -400,7 +409,7 @@ size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N
 ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
                            void* workspace, size_t workspace_bytes, void* stream)
 {
-    if (!args || idx < 0 || idx >= mx_registry_count())
+    if (!args || idx < 0 || idx >= mx_registry_total())
         return fail(GA_ERR_ARG, "kernel_launch: bad kernel index %d", idx);
     const MxKernel& k = g_mx_kernels[idx];
     const int M = (int)args->M, N = (int)args->N, K = (int)args->K;
