@@ -184,4 +184,25 @@ __device__ __forceinline__ int mx_scale_exp(float amax, int rule)
     return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 
+// Workgroup (x, y) -> (tile_m, tile_n). Workgroup ids are dispatched
+// round-robin over the 8 XCDs; the remap gives each XCD a contiguous range of
+// tiles, swept column by column inside groups of `group_m` M-tiles so the
+// workgroups resident on one XCD share A and B panels in its L2.
+__device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int group_m, int& tm,
+                                         int& tn)
+{
+    const int total = gdx * gdy;
+    int lin = by * gdx + bx;
+    const int full = (total / 8) * 8;
+    if (lin < full)
+        lin = (lin % 8) * (total / 8) + lin / 8;
+    const int per_group = group_m * gdx;
+    const int g = lin / per_group;
+    const int first_m = g * group_m;
+    const int gsize = min(gdy - first_m, group_m);
+    const int r = lin - g * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
 } // namespace ga

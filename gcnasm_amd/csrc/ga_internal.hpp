@@ -29,6 +29,11 @@ struct MxKernel {
     ga_tile_config cfg;
     mx_launch_fn launch;
 };
+// 256x256 eight-wave kernels (gemm_mx_pp.hip), preshuffled / plain B.
+void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                      hipStream_t stream);
+void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                        hipStream_t stream);
 int mx_registry_count();  // manifest rows
 int mx_registry_total();  // manifest rows + kernels reachable only by name
 const MxKernel* mx_registry_get(int idx);

@@ -70,24 +70,6 @@ struct MxCfg {
 
 constexpr int kGroupM = 4; // M-tiles per L2 group
 
-// Workgroup (x, y) -> (tile_m, tile_n): XCD-contiguous ranges, then column
-// sweeps inside groups of kGroupM M-tiles.
-__device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int& tm, int& tn)
-{
-    const int total = gdx * gdy;
-    int lin = by * gdx + bx;
-    const int full = (total / 8) * 8;
-    if (lin < full)
-        lin = (lin % 8) * (total / 8) + lin / 8;
-    const int per_group = kGroupM * gdx;
-    const int g = lin / per_group;
-    const int first_m = g * kGroupM;
-    const int gsize = min(gdy - first_m, kGroupM);
-    const int r = lin - g * per_group;
-    tm = first_m + r % gsize;
-    tn = r / gsize;
-}
-
 template <class C>
 struct MxState {
     __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
@@ -178,7 +160,7 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
     int tile_m, tile_n;
-    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, tile_m, tile_n);
+    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, kGroupM, tile_m, tile_n);
     const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
 
     const int z = blockIdx.z, gdz = gridDim.z;
@@ -346,6 +328,14 @@ static const MxKernel g_mx_kernels[] = {
     // not in the manifest
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 2, 0, "_ns2"),
+    {{256, 256, 0, 1, "ga_mxfp8_bf16_BpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256.co"},
+     &launch_mx_pp_bps},
+    {{256, 256, 1, 1, "ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
+      "ga_mxfp8_bf16_BpreShuffle_256x256_splitK.co"},
+     &launch_mx_pp_bps},
+    {{256, 256, 0, 0, "ga_mxfp8_bf16_noBpreShuffle_256x256",
+      "ga_mxfp8_bf16_noBpreShuffle_256x256.co"},
+     &launch_mx_pp_nobps},
 };
 constexpr int kManifestCount = 13;
 

@@ -1,0 +1,422 @@
+// gemm_mx_pp.hip -- 256x256 MXFP8 GEMM tile for large M and N (f4gemm ABI).
+//
+// Same contract as the 4-wave kernels of gemm_mx.hip (operands, shuffled
+// scales, optional preshuffled B, split-K into an fp32 workspace); this file
+// holds the high-throughput tile. Design:
+//  * 512 threads = 8 waves in two groups. Wave w sits on SIMD w % 4, so each
+//    SIMD runs one wave of each group. The groups execute the same program
+//    offset by one barrier: while one group issues MFMAs (at raised issue
+//    priority), the other does its LDS reads and global->LDS copies, and they
+//    swap at every workgroup barrier, so the MFMA pipe of every SIMD is fed
+//    by one wave while the other wave's memory work overlaps it.
+//  * The 256x256 C tile is four 128x128 quadrants. In each quadrant a wave
+//    owns 64 rows (by group) x 32 columns (by SIMD): 4 x 2 MFMA tiles of
+//    16x16, 8 MFMAs of 16x16x128 per quadrant per K step, 128 accumulator
+//    VGPRs in all.
+//  * One K step (128) is four phases, one quadrant each (00, 01, 10, 11).
+//    Each phase reads ONE operand fragment (A rows of an M half, or B columns
+//    of an N half: A0, B1, A1, then B0 of the next step) and multiplies it
+//    with the fragment kept from the previous phase; the read overlaps the
+//    other group's MFMA slot.
+//  * LDS: A and B each hold two K-step slots of two 16 KB half tiles, plus a
+//    ring of three 4 KB scale slots: 140 KB. A half tile is refilled with the
+//    step two ahead once both groups have read it, so its copy has six phases
+//    to land; every phase ends with a counted vmcnt wait on the copy the next
+//    phase reads.
+//  * Row-major operands (A, and B without preshuffle) sit in LDS as 128-byte
+//    rows, 16-byte K chunk c of row r at slot c ^ ((r >> 1) & 7). Each copy
+//    instruction then reads 8 whole 128-byte rows (whole cache lines; a copy
+//    touching 16 rows x 64 bytes moves half the bytes per request), and the
+//    MFMA operand reads (lane 16g + r: row r, chunks g and g + 4) hit 64
+//    distinct banks per 16 lanes.
+//  * Preshuffled B keeps its global byte order in LDS: [K/16:8][row:16][16 B]
+//    per 16-row group, so a copy is 1 KB contiguous and MFMA operand half h of
+//    lane l is the 16 B at h*1024 + l*16.
+//  * Addressing is kept out of VGPRs: one VGPR base per operand for the LDS
+//    reads (slot and half are compile-time ds_read offsets) and one per
+//    operand for the copies (uniform parts added from SGPRs).
+#include "ga_device.hpp"
+#include "ga_internal.hpp"
+
+namespace ga {
+namespace {
+
+constexpr int kNT = 512;
+constexpr int kHalf = 16384;  // 128 rows x 128 K of fp8
+constexpr int kOpSlot = 2 * kHalf;
+constexpr int kARegion = 0;   // A: [slot][half] half tiles
+constexpr int kBRegion = 2 * kOpSlot;
+constexpr int kScaleSlot = 16 * 256; // 8 A + 8 B shuffled 32-row scale blocks
+constexpr int kScaleBase = 4 * kOpSlot;
+constexpr int kLds = kScaleBase + 3 * kScaleSlot;
+static_assert(kLds <= 160 * 1024, "LDS budget");
+constexpr int kPpGroupM = 4;
+
+struct PpLoad {
+    __amdgpu_buffer_rsrc_t ra, rb, rs;
+    uint32_t va, vb, vs;   // per-lane copy offsets (half 0, copy 0, first K step)
+    uint32_t a_hstep;      // A bytes between copies 0 and 1 of a half (64 rows)
+    uint32_t b_hstep;      // same for B
+    uint32_t b_kstep;      // B bytes per 128-K step
+    uint32_t s_blk;        // scale bytes between this wave's two blocks
+};
+
+// Uniform byte offset as an SGPR operand, kept opaque so the per-copy
+// address is formed at the copy (one VGPR base per operand, no hoisted
+// per-copy VGPRs).
+__device__ __forceinline__ uint32_t uni(uint32_t x)
+{
+    return __builtin_amdgcn_readfirstlane(x);
+}
+
+__device__ __forceinline__ void wait_lds_barrier()
+{
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// Copies (2 per wave) of A half tile h of K step t.
+__device__ __forceinline__ void issue_a(const PpLoad& L, char* smem, int h, int t, int wave)
+{
+    char* dst = smem + kARegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
+    const uint32_t o = (uint32_t)h * 2 * L.a_hstep + (uint32_t)t * 128;
+    lds_load16(L.ra, (lds_void*)dst, L.va + uni(o), 0);
+    lds_load16(L.ra, (lds_void*)(dst + 8192), L.va + uni(o + L.a_hstep), 0);
+}
+
+__device__ __forceinline__ void issue_b(const PpLoad& L, char* smem, int h, int t, int wave)
+{
+    char* dst = smem + kBRegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
+    const uint32_t o = (uint32_t)h * 2 * L.b_hstep + (uint32_t)t * L.b_kstep;
+    lds_load16(L.rb, (lds_void*)dst, L.vb + uni(o), 0);
+    lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb + uni(o + L.b_hstep), 0);
+}
+
+// Scales of K step t into ring slot `ring`: wave w copies blocks 2w, 2w+1
+// (blocks 0-7: A rows, 8-15: B rows). A shuffled dword covers 256 K.
+__device__ __forceinline__ void issue_s(const PpLoad& L, char* smem, int t, int ring, int wave)
+{
+    char* dst = smem + kScaleBase + ring * kScaleSlot + wave * 512;
+    const uint32_t q = (uint32_t)(t >> 1) * 256;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4, L.vs + uni(q), 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + 256), 4,
+                                             L.vs + uni(q + L.s_blk), 0, 0, 0);
+}
+
+__device__ __forceinline__ v8i lds_frag(const char* p0, const char* p1)
+{
+    v4i x0 = *(const v4i*)p0;
+    v4i x1 = *(const v4i*)p1;
+    return (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+}
+
+// Per-lane LDS read bases. Swizzled row-major operand: lane 16g + r reads
+// row r, chunks g (at o) and g + 4 (at o ^ 64; adding multiples of 128 keeps
+// bit 6, so the XOR commutes with the block offsets).
+struct ReadBase {
+    const char* a0;
+    const char* a1;
+    const char* b0;
+    const char* b1;
+    const char* sa;
+    const char* sb;
+};
+
+// A fragment of slot `slot`, half H: rows H*128 + grp*64 + [0, 64).
+template <int H>
+__device__ __forceinline__ void read_a(const ReadBase& rb, int slot, v8i (&a)[4])
+{
+    const int off = kARegion + slot * kOpSlot + H * kHalf;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        a[i] = lds_frag(rb.a0 + off + i * 2048, rb.a1 + off + i * 2048);
+}
+
+// B fragment of slot `slot`, half H: columns H*128 + simd*32 + [0, 32).
+template <int H>
+__device__ __forceinline__ void read_b(const ReadBase& rb, int slot, v8i (&b)[2])
+{
+    const int off = slot * kOpSlot + H * kHalf; // base includes the B region
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        b[t] = lds_frag(rb.b0 + off + t * 2048, rb.b1 + off + t * 2048);
+}
+
+// Scale dwords of ring slot `ring`. Byte 2*d4 + d1 of a dword holds 128-K
+// half d4 (the step's parity) of 16-row half d1; the shift by `sh` (16 for
+// odd steps) moves this step's half to bytes 0-1.
+template <int H>
+__device__ __forceinline__ void read_sa(const ReadBase& rb, int ring, uint32_t sh,
+                                        uint32_t (&s)[2])
+{
+    const char* p = rb.sa + ring * kScaleSlot + H * 4 * 256;
+    s[0] = *(const uint32_t*)p >> sh;
+    s[1] = *(const uint32_t*)(p + 256) >> sh;
+}
+
+template <int H>
+__device__ __forceinline__ uint32_t read_sb(const ReadBase& rb, int ring, uint32_t sh)
+{
+    return *(const uint32_t*)(rb.sb + ring * kScaleSlot + H * 4 * 256) >> sh;
+}
+
+// One quadrant: 4 A tiles x 2 B tiles; the scale byte is 2*P + (16-row
+// half inside the 32-row scale block).
+template <int P>
+__device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4],
+                                             const v8i (&b)[2], const uint32_t (&sa)[2],
+                                             uint32_t sb)
+{
+    __builtin_amdgcn_s_setprio(1);
+    static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<2>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            acc[i][t] = mfma_mx16<2 * P + (t & 1), 2 * P + (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+                                                                    (int)sa[i >> 1]);
+        });
+    });
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// Phase boundary: own copies waited for (count = copies issued after the
+// ones the next phase reads), then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void phase_sync()
+{
+    wait_vmcnt<N>();
+    wait_lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__device__ __forceinline__ void slot_sync()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool BPS>
+__global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
+void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[kLds];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, simd = wave & 3;
+    const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+    int tile_m, tile_n;
+    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, kPpGroupM, tile_m, tile_n);
+    const int m0 = tile_m * 256, n0 = tile_n * 256;
+
+    const int z = blockIdx.z, gdz = gridDim.z;
+    int kpt = K;
+    if (gdz > 1)
+        kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
+    const int kb = z * kpt;
+    const int ke = min(K, kb + kpt);
+    const int nsteps = (ke - kb) / 128;
+
+    v4f acc[4][4][2];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+                acc[q][i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    if (nsteps > 0) {
+        const uint32_t lda = args.stride_A0, ldb = args.stride_B0;
+        PpLoad L;
+        // Copy c of a row-major half tile writes LDS bytes c*8192 + wave*1024
+        // + lane*16 = row c*64 + wave*8 + lane/8, slot lane%8, which holds K
+        // chunk slot ^ ((row >> 1) & 7); the chunk does not depend on c or
+        // the half (64 and 128 rows keep (row >> 1) & 7).
+        const int crow = wave * 8 + (lane >> 3);
+        const int ckc = (lane & 7) ^ ((crow >> 1) & 7);
+        {
+            const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
+            long long abytes = (long long)(M - m0) * lda;
+            L.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+            L.va = (uint32_t)crow * lda + ckc * 16 + (uint32_t)kb;
+            L.a_hstep = 64 * lda;
+            if (BPS) {
+                // preshuffled B: each 16-row group is K*16 contiguous bytes,
+                // [K/16][16 rows][16 B]; one K step is 2 KB of it. Copy c of
+                // half h: groups h*8 + c*4 + wave/2, bytes (wave&1)*1024 + lane*16.
+                const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
+                long long bbytes = (long long)(N - n0) * K;
+                L.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+                L.b_kstep = 2048;
+                L.b_hstep = 4 * (uint32_t)K * 16;
+                L.vb = (uint32_t)(wave >> 1) * (uint32_t)K * 16 + (wave & 1) * 1024 + lane * 16 +
+                       (uint32_t)kb * 16;
+            } else {
+                const char* pb = (const char*)args.ptr_B + (size_t)n0 * ldb;
+                long long bbytes = (long long)(N - n0) * ldb;
+                L.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+                L.b_kstep = 128;
+                L.b_hstep = 64 * ldb;
+                L.vb = (uint32_t)crow * ldb + ckc * 16 + (uint32_t)kb;
+            }
+            // scales: shuffled layout, 256-byte block per (32 rows, 256 K);
+            // wave w copies blocks 2w, 2w+1 of the tile's 16 (A 0-7, B 8-15)
+            const bool sb = wave >= 4;
+            const uint32_t sn = sb ? args.stride_ScaleB0 : args.stride_ScaleA0;
+            const int rows = sb ? N : M;
+            const int base = sb ? n0 : m0;
+            L.rs = make_rsrc(sb ? args.ptr_ScaleB : args.ptr_ScaleA,
+                             (uint32_t)((rows + 31) / 32 * 32) * sn);
+            const int blk = (wave & 3) * 2;
+            L.vs = ((uint32_t)((base + blk * 32) / 32) * (sn / 8) + (uint32_t)(kb / 256)) * 256 +
+                   lane * 4;
+            L.s_blk = (sn / 8) * 256;
+        }
+
+        ReadBase rb;
+        {
+            const uint32_t r = lane & 15, g = lane >> 4;
+            const uint32_t o = r * 128 + ((g ^ ((r >> 1) & 7)) * 16);
+            rb.a0 = smem + grp * 64 * 128 + o;
+            rb.a1 = smem + grp * 64 * 128 + (o ^ 64u);
+            if (BPS) {
+                rb.b0 = smem + kBRegion + simd * 32 * 128 + lane * 16;
+                rb.b1 = rb.b0 + 1024;
+            } else {
+                rb.b0 = smem + kBRegion + simd * 32 * 128 + o;
+                rb.b1 = smem + kBRegion + simd * 32 * 128 + (o ^ 64u);
+            }
+            rb.sa = smem + kScaleBase + grp * 2 * 256 + lane * 4;
+            rb.sb = smem + kScaleBase + (8 + simd) * 256 + lane * 4;
+        }
+
+        // Operand fragments: rows of one A half, B columns of N half 0 / 1,
+        // with their scale dwords.
+        v8i fa[4], fb0[2], fb1[2];
+        uint32_t sa[2], sb0, sb1;
+
+        // Prologue: the copies a steady pipeline would have issued before
+        // step 0, in the same order (B0+S, A0, B1, A1 of step 0; B0+S, A0, B1
+        // of step 1), then the read of the phase before step 0 (B0).
+        issue_b(L, smem, 0, 0, wave);
+        issue_s(L, smem, 0, 0, wave);
+        issue_a(L, smem, 0, 0, wave);
+        issue_b(L, smem, 1, 0, wave);
+        issue_a(L, smem, 1, 0, wave);
+        issue_b(L, smem, 0, 1, wave);
+        issue_s(L, smem, 1, 1, wave);
+        issue_a(L, smem, 0, 1, wave);
+        issue_b(L, smem, 1, 1, wave);
+        phase_sync<14>(); // B0 + scales of step 0
+        read_b<0>(rb, 0, fb0);
+        sb0 = read_sb<0>(rb, 0, 0);
+        phase_sync<12>(); // A0 of step 0
+        if (grp == 1)
+            slot_sync(); // second group runs one barrier behind
+
+        // One K step s of parity P (LDS slot P). A memory slot issues its
+        // copy (a half tile two steps ahead, into a half both groups have
+        // finished reading) before its LDS reads, then waits for the copy
+        // the next phase reads:
+        //   phase  read        copy           quadrant   younger copies
+        //   1      A0(s)       A1(s+1)        00         12
+        //   2      B1(s)       B0+S(s+2)      01         14
+        //   3      A1(s)       A0(s+2)        10         12
+        //   4      B0(s+1)     B1(s+2)        11         12
+        int r0 = 0; // scale ring slot of step s
+        for (int s = 0; s < nsteps; s++) {
+            const int P = s & 1;
+            const uint32_t sh = (uint32_t)P * 16, sh1 = (uint32_t)(P ^ 1) * 16;
+            const int r1 = r0 == 2 ? 0 : r0 + 1;
+            const int r2 = r1 == 2 ? 0 : r1 + 1;
+            // phase 1
+            issue_a(L, smem, 1, s + 1, wave);
+            read_sa<0>(rb, r0, sh, sa);
+            read_a<0>(rb, P, fa);
+            phase_sync<12>();
+            mma_quadrant<0>(acc[0], fa, fb0, sa, sb0);
+            slot_sync();
+            // phase 2
+            issue_b(L, smem, 0, s + 2, wave);
+            issue_s(L, smem, s + 2, r2, wave);
+            sb1 = read_sb<1>(rb, r0, sh);
+            read_b<1>(rb, P, fb1);
+            phase_sync<14>();
+            mma_quadrant<0>(acc[1], fa, fb1, sa, sb1);
+            slot_sync();
+            // phase 3
+            issue_a(L, smem, 0, s + 2, wave);
+            read_sa<1>(rb, r0, sh, sa);
+            read_a<1>(rb, P, fa);
+            phase_sync<12>();
+            mma_quadrant<0>(acc[2], fa, fb0, sa, sb0);
+            slot_sync();
+            // phase 4
+            issue_b(L, smem, 1, s + 2, wave);
+            sb0 = read_sb<0>(rb, r1, sh1);
+            read_b<0>(rb, P ^ 1, fb0);
+            phase_sync<12>();
+            mma_quadrant<0>(acc[3], fa, fb1, sa, sb1);
+            slot_sync();
+            r0 = r1;
+        }
+        if (grp == 0)
+            slot_sync(); // matches the second group's extra barrier
+        wait_vmcnt<0>(); // copies of steps past the slice land before exit
+    }
+
+    // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile. The library is
+    // built with -ffp-contract=off: alpha*v and + beta*c round separately.
+    const int ldd = (int)args.stride_C0;
+    const float alpha = args.alpha, beta = args.beta;
+    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + (q >> 1) * 128 + grp * 64 + i * 16 + (lane & 15);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int n = n0 + (q & 1) * 128 + simd * 32 + t * 16 + (lane >> 4) * 4;
+                if (m >= M || n >= N)
+                    continue;
+                const v4f v = acc[q][i][t];
+                if (gdz > 1) {
+                    *(v4f*)(ws + ((size_t)z * M + m) * N + n) = v;
+                } else {
+                    uint16_t o[4];
+                    const uint16_t* cin =
+                        use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n : nullptr;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float x = alpha * v[j];
+                        if (use_c)
+                            x = x + beta * bf16_to_f32(cin[j]);
+                        o[j] = f32_to_bf16(x);
+                    }
+                    uint2 pk;
+                    pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                    pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                    *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+                }
+            }
+        }
+    }
+}
+
+} // namespace
+
+void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                      hipStream_t stream)
+{
+    hipLaunchKernelGGL(mx_pp_kernel<true>, dim3(gdx, gdy, gdz), dim3(kNT), 0, stream, args, ws);
+}
+
+void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                        hipStream_t stream)
+{
+    hipLaunchKernelGGL(mx_pp_kernel<false>, dim3(gdx, gdy, gdz), dim3(kNT), 0, stream, args, ws);
+}
+
+} // namespace ga

@@ -10,6 +10,7 @@ the north-star rule in helpers.bf16_compare, with the MFMA truncation bound
 (helpers.MFMA_BOUND_FACTOR) for outputs that cancel.
 """
 import ctypes
+import re
 
 import numpy as np
 import pytest
@@ -64,10 +65,20 @@ def check(got, want, label, absdot):
 
 
 def cfg_named(name):
+    """Manifest row of `name`, or for kernels reachable only by name
+    (ga_kernel_find) a row built from the tile encoded in the name."""
     for c in f4gemm.manifest():
         if c.knl_name == name:
             return c
-    raise KeyError(name)
+    m = re.search(r"_(\d+)x(\d+)", name)
+    return f4gemm.Config(int(m.group(1)), int(m.group(2)), int("_splitK" in name),
+                         int("noBpreShuffle" not in name), name, name + ".co")
+
+
+# Kernels outside the manifest, reachable by name.
+NAMED_ONLY = ["ga_mxfp8_bf16_BpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
+              "ga_mxfp8_bf16_noBpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256_ns2",
+              "ga_mxfp8_bf16_BpreShuffle_256x128_ns2"]
 
 
 def test_config1_heuristic(dev):
@@ -107,8 +118,24 @@ def test_every_kernel(dev, name):
     check(got, expect(qa, sa, qb, sb, 0), name, oracle.mx_absdot(qa, sa, qb, sb))
 
 
+@pytest.mark.parametrize("name", NAMED_ONLY)
+@pytest.mark.parametrize("shape", [(300, 2048, 1024), (520, 784, 1536), (256, 256, 128),
+                                   (1, 256, 256), (777, 1040, 2048)])
+def test_named_only_kernels(dev, name, shape):
+    """Kernels outside the manifest; shapes cover partial M and N tiles, a
+    single K step and a single row."""
+    M, N, K = shape
+    cfg = cfg_named(name)
+    assert cfg not in f4gemm.manifest()
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M + 7 * N + K)
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0)
+    check(got, expect(qa, sa, qb, sb, 0), "%s %s" % (name, shape),
+          oracle.mx_absdot(qa, sa, qb, sb))
+
+
 @pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x128_splitK",
-                                  "ga_mxfp8_bf16_BpreShuffle_32x256_splitK"])
+                                  "ga_mxfp8_bf16_BpreShuffle_32x256_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_256x256_splitK"])
 @pytest.mark.parametrize("l2", [1, 2, 3, 4])
 def test_splitk(dev, name, l2):
     M, N, K = 256, 1024, 4096
