@@ -64,6 +64,14 @@ __device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t vof
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
 
+// Streaming variant for data read once: the non-temporal cache policy bit
+// (gfx950 "nt") so the stream does not evict reused lines.
+__device__ __forceinline__ v4i buf_load16_stream(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                 uint32_t soff)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
+}
+
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
 {
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);

@@ -304,40 +304,39 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, false}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
 // Manifest order matters: the heuristic breaks ties by it. Entries after
 // kManifestCount are found by name (ga_kernel_find) but are not offered to the
 // heuristic.
+#define GA_MX_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                 \
+    {{256, 256, SPLIT, BPS, "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
+      "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
+     &FN, true}
+
 static const MxKernel g_mx_kernels[] = {
+    GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
     GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 0, ""),
     GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
     GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 0, ""),
+    GA_MX_PP_ENTRY(1, 1, "_splitK", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 1, "_splitK"),
     GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 1, "_splitK"),
     GA_MX_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
+    GA_MX_PP_ENTRY(0, 0, "", launch_mx_pp_nobps),
     GA_MX_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
     GA_MX_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
-    // not in the manifest
+    // not in the manifest: the 4-wave 256x256 tile (two stages)
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
-    GA_MX_ENTRY(256, 128, 2, 2, 1, 2, 0, "_ns2"),
-    {{256, 256, 0, 1, "ga_mxfp8_bf16_BpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256.co"},
-     &launch_mx_pp_bps},
-    {{256, 256, 1, 1, "ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
-      "ga_mxfp8_bf16_BpreShuffle_256x256_splitK.co"},
-     &launch_mx_pp_bps},
-    {{256, 256, 0, 0, "ga_mxfp8_bf16_noBpreShuffle_256x256",
-      "ga_mxfp8_bf16_noBpreShuffle_256x256.co"},
-     &launch_mx_pp_nobps},
 };
-constexpr int kManifestCount = 13;
+constexpr int kManifestCount = 16;
 
 int mx_registry_count() { return kManifestCount; }
 int mx_registry_total() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
@@ -433,6 +432,16 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
             return fail(GA_ERR_ARG, "gdz=%d does not match log2_k_split=%d", gdz, L);
     }
     hipStream_t s = (hipStream_t)stream;
+    if (k.small_m_stream && mx_decode_applies(*args, gdz)) {
+        // few rows: stream B, K slices summed inside the kernel (no workspace)
+        int num_cu = 0;
+        ga_status st = device_cu_count(&num_cu);
+        if (st != GA_OK)
+            return st;
+        launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, num_cu, s);
+        GA_HIP_CHECK(hipGetLastError());
+        return GA_OK;
+    }
     float* ws = nullptr;
     if (gdz > 1) {
         size_t need = (size_t)gdz * M * N * sizeof(float);

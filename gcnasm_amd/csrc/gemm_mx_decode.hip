@@ -1,0 +1,274 @@
+// gemm_mx_decode.hip -- MXFP8 GEMM for small M (decode), HBM-streaming.
+//
+// Used by the 256x256 manifest kernels when M <= 64: with so few rows the GEMM
+// is a stream over B (N x K bytes), so the design is about keeping HBM busy:
+//  * one wave per NG 16-column groups of B and one K slice; B's 2 KB per
+//    group and 128-K step (two 1 KB contiguous runs in the preshuffled
+//    layout) goes straight from memory into the MFMA operand registers;
+//  * a ring of D steps of loads in flight per wave (24 KB of B for M <= 16);
+//  * the A rows (<= 64, L2-resident) are loaded the same way, once per step
+//    for all NG groups, and multiply B with v_mfma_scale_f32_16x16x128_f8f6f4,
+//    one MFMA per 16 rows per group per step;
+//  * split-K: the gdz K slices of a column group run in waves of the same
+//    workgroup and are summed in LDS in slice order (slice 0 first), the
+//    order the split-K reduce uses, so no workspace is needed;
+//  * workgroup = T column tasks x KS slices (T * KS = 4 waves, or KS waves
+//    for KS = 8).
+#include "ga_device.hpp"
+#include "ga_internal.hpp"
+#include <algorithm>
+
+namespace ga {
+namespace {
+
+template <int TM, int NG_>
+struct DecCfg {
+    static constexpr int NG = NG_; // 16-column groups per wave
+    static constexpr int D = TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
+};
+
+// Uniform byte offsets as SGPR operands.
+__device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+template <int TM, int NG_, bool BPS>
+__global__ __attribute__((amdgpu_flat_work_group_size(64, 512)))
+void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
+{
+    constexpr int D = DecCfg<TM, NG_>::D, NG = NG_, NB = NG; // one scale dword per group
+    constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
+    constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
+    static_assert(kLoadsPerStep * (D - 1) < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) float red[8 * NG * TM * 256]; // <= 8 waves
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slice = wave % ks, tl = wave / ks;
+    const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+    // Workgroup b owns 16-column groups [b*G/nwg, (b+1)*G/nwg): equal shares
+    // (within one group) for every CU; its waves take NG groups each.
+    const int ngroups = N / 16;
+    const int g_end = (int)(((long long)(blockIdx.x + 1) * ngroups) / nwg);
+    const int cg0 = (int)(((long long)blockIdx.x * ngroups) / nwg) + tl * NG;
+    const int ng_here = min(NG, g_end - cg0); // groups past it read as zero
+    const bool live = ng_here > 0;
+
+    int kpt = K;
+    if (ks > 1)
+        kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
+    const int kb = slice * kpt;
+    const int ke = min(K, kb + kpt);
+    const int nsteps = live ? max(0, (ke - kb) / 128) : 0;
+
+    v4f acc[NG][TM];
+#pragma unroll
+    for (int c = 0; c < NG; c++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    if (nsteps > 0) {
+        const int r = lane & 15, g = lane >> 4;
+        const uint32_t lda = args.stride_A0;
+        long long abytes = (long long)M * lda;
+        const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+        // A: lane 16g + r reads row 16i + r, K chunks g and g + 4 of the step
+        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kb;
+        // B: groups past N read as zero (range-checked buffer)
+        __amdgpu_buffer_rsrc_t rbuf;
+        uint32_t vb, b_step, b_hi, b_grp;
+        if (BPS) {
+            // group cg: K*16 contiguous bytes, [K/16][16 rows][16 B]
+            const char* pb = (const char*)args.ptr_B + (size_t)cg0 * K * 16;
+            rbuf = make_rsrc(pb, (uint32_t)ng_here * (uint32_t)K * 16);
+            vb = (uint32_t)lane * 16 + (uint32_t)kb * 16;
+            b_step = 2048;
+            b_hi = 1024;
+            b_grp = (uint32_t)K * 16;
+        } else {
+            const uint32_t ldb = args.stride_B0;
+            const char* pb = (const char*)args.ptr_B + (size_t)cg0 * 16 * ldb;
+            rbuf = make_rsrc(pb, (uint32_t)ng_here * 16 * ldb);
+            vb = (uint32_t)r * ldb + g * 16 + (uint32_t)kb;
+            b_step = 128;
+            b_hi = 64;
+            b_grp = 16 * ldb;
+        }
+        // scales: shuffled dword of lane l covers (row l%16 + 16 h, K block
+        // l/16) for 256 K; byte 2*(step parity) + h
+        const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
+        const auto rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)((M + 31) / 32 * 32) * sna);
+        const auto rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)((N + 31) / 32 * 32) * snb);
+        const uint32_t vsa = ((uint32_t)(kb / 256)) * 256 + lane * 4;
+        // group cg uses byte (cg & 1) of 32-row block cg/2
+        uint32_t vsb[NG];
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+            vsb[c] = ((uint32_t)((cg0 + c) / 2) * (snb / 8) + (uint32_t)(kb / 256)) * 256 + lane * 4;
+        const uint32_t sa_blk = (sna / 8) * 256;
+
+        v8i fb[D][NG];
+        v8i fa[D][TM];
+        uint32_t fsa[D][SA], fsb[D][NB];
+
+        auto load = [&](int s, auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t ob = (uint32_t)s * b_step;
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                v4i x0 = buf_load16_stream(rbuf, vb + uni(ob + c * b_grp), 0);
+                v4i x1 = buf_load16_stream(rbuf, vb + uni(ob + c * b_grp + b_hi), 0);
+                fb[j][c] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t oa = (uint32_t)s * 128 + (uint32_t)i * 16 * lda;
+                v4i y0 = buf_load16(ra, va + uni(oa), 0);
+                v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
+                fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+            }
+            const uint32_t q = (uint32_t)(s >> 1) * 256;
+#pragma unroll
+            for (int h = 0; h < SA; h++)
+                fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+                fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+        };
+        auto mma = [&](int s, auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t sh = (uint32_t)(s & 1) * 16;
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                const uint32_t sb = fsb[j][c] >> (sh + 8 * ((cg0 + c) & 1));
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const uint32_t sa = fsa[j][i >> 1] >> (sh + 8 * (i & 1));
+                    acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb, (int)sa);
+                }
+            }
+        };
+
+        // The loads of each step stay in issue order (slot 0 oldest), so the
+        // wait before step s+J's MFMAs lets the D-1 younger steps fly.
+        static_for<D>([&](auto J) {
+            load(min((int)J, nsteps - 1), J);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        int s = 0;
+        for (; s + D <= nsteps; s += D) {
+            static_for<D>([&](auto J) {
+                wait_vmcnt<kLoadsPerStep * (D - 1)>();
+                mma(s + J, J);
+                load(min(s + D + (int)J, nsteps - 1), J);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        static_for<D>([&](auto J) {
+            if ((int)J < nsteps - s)
+                mma(s + J, J);
+        });
+    }
+
+    // Sum the K slices of each column group in slice order, then the epilogue
+    // (lane holds C[m][n .. n+3], m = 16i + lane%16, n = 16cg + 4(lane/16)).
+    if (ks > 1) {
+        float* mine = red + ((tl * ks + slice) * NG * TM) * 256;
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                *(v4f*)(mine + (c * TM + i) * 256 + lane * 4) = acc[c][i];
+        __syncthreads();
+        if (slice != 0)
+            return;
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                v4f t = *(const v4f*)(mine + (c * TM + i) * 256 + lane * 4);
+                for (int z = 1; z < ks; z++) {
+                    const v4f u =
+                        *(const v4f*)(mine + ((z * NG + c) * TM + i) * 256 + lane * 4);
+                    t = t + u;
+                }
+                acc[c][i] = t;
+            }
+    }
+    if (!live)
+        return;
+    const int ldd = (int)args.stride_C0;
+    const float alpha = args.alpha, beta = args.beta;
+    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+        if (c >= ng_here)
+            continue;
+        const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = i * 16 + (lane & 15);
+            if (m >= M)
+                continue;
+            const v4f v = acc[c][i];
+            uint16_t o[4];
+            const uint16_t* cin =
+                use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n : nullptr;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float x = alpha * v[j];
+                if (use_c)
+                    x = x + beta * bf16_to_f32(cin[j]);
+                o[j] = f32_to_bf16(x);
+            }
+            uint2 pk;
+            pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+            pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+            *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+        }
+    }
+}
+
+// Workgroups: one per CU (more when a CU's share needs over 8 waves), each
+// with ceil(share / NG) column tasks x ks slices.
+template <int TM, int NG, bool BPS>
+void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t stream)
+{
+    const int groups = (int)args.N / 16;
+    const int max_tasks = 8 / ks; // waves per workgroup <= 8
+    int nwg = std::min(num_cu, (groups + NG - 1) / NG);
+    nwg = std::max(nwg, (groups + NG * max_tasks - 1) / (NG * max_tasks));
+    const int share = (groups + nwg - 1) / nwg;
+    const int tasks = (share + NG - 1) / NG;
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS>), dim3(nwg), dim3(64 * tasks * ks), 0, stream,
+                       args, nwg, ks);
+}
+
+} // namespace
+
+bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz)
+{
+    return args.M >= 1 && args.M <= 64 && gdz <= 8;
+}
+
+void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, int num_cu,
+                      hipStream_t stream)
+{
+    const int tm = ((int)args.M + 15) / 16;
+    if (bps) {
+        if (tm == 1)
+            launch_dec<1, 2, true>(args, gdz, num_cu, stream);
+        else if (tm == 2)
+            launch_dec<2, 2, true>(args, gdz, num_cu, stream);
+        else
+            launch_dec<4, 2, true>(args, gdz, num_cu, stream);
+    } else {
+        if (tm == 1)
+            launch_dec<1, 2, false>(args, gdz, num_cu, stream);
+        else if (tm == 2)
+            launch_dec<2, 2, false>(args, gdz, num_cu, stream);
+        else
+            launch_dec<4, 2, false>(args, gdz, num_cu, stream);
+    }
+}
+
+} // namespace ga

@@ -76,9 +76,12 @@ def cfg_named(name):
 
 
 # Kernels outside the manifest, reachable by name.
-NAMED_ONLY = ["ga_mxfp8_bf16_BpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
-              "ga_mxfp8_bf16_noBpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256_ns2",
-              "ga_mxfp8_bf16_BpreShuffle_256x128_ns2"]
+NAMED_ONLY = ["ga_mxfp8_bf16_BpreShuffle_256x256_ns2"]
+
+# The 256x256 eight-wave tiles, run on shapes with partial tiles, a single K
+# step and one row.
+PP_KERNELS = ["ga_mxfp8_bf16_BpreShuffle_256x256", "ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
+              "ga_mxfp8_bf16_noBpreShuffle_256x256"]
 
 
 def test_config1_heuristic(dev):
@@ -118,15 +121,15 @@ def test_every_kernel(dev, name):
     check(got, expect(qa, sa, qb, sb, 0), name, oracle.mx_absdot(qa, sa, qb, sb))
 
 
-@pytest.mark.parametrize("name", NAMED_ONLY)
+@pytest.mark.parametrize("name", NAMED_ONLY + PP_KERNELS)
 @pytest.mark.parametrize("shape", [(300, 2048, 1024), (520, 784, 1536), (256, 256, 128),
                                    (1, 256, 256), (777, 1040, 2048)])
-def test_named_only_kernels(dev, name, shape):
-    """Kernels outside the manifest; shapes cover partial M and N tiles, a
-    single K step and a single row."""
+def test_large_tiles_edge_shapes(dev, name, shape):
+    """Large tiles (in the manifest or found by name only) on shapes with
+    partial M and N tiles, a single K step and a single row."""
     M, N, K = shape
     cfg = cfg_named(name)
-    assert cfg not in f4gemm.manifest()
+    assert (cfg in f4gemm.manifest()) == (name not in NAMED_ONLY)
     qa, sa, qb, sb = mx_operands(M, N, K, seed=M + 7 * N + K)
     got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0)
     check(got, expect(qa, sa, qb, sb, 0), "%s %s" % (name, shape),
@@ -211,3 +214,36 @@ def test_one_call_mxfp8_gemm_from_float(dev):
     got = D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
     check(got, expect(qa, sa, qb, sb, ld.log2_k_split), "one-call",
           oracle.mx_absdot(qa, sa, qb, sb))
+
+
+# Small-M streaming path of the 256x256 kernels: every M row tile count
+# (M = 1, 16, 17, 33, 64), odd 16-column group counts (N = 784 -> 49 groups),
+# K not a multiple of 256, and each split factor the path handles in-kernel.
+@pytest.mark.parametrize("M", [1, 16, 17, 33, 64])
+@pytest.mark.parametrize("NKL", [(784, 1152, 0), (784, 1152, 1), (4096, 2048, 0),
+                                 (4096, 2048, 1), (4096, 2048, 2), (4096, 2048, 3),
+                                 (1808, 3072, 2)])
+def test_decode_path(dev, M, NKL):
+    N, K, l2 = NKL
+    name = "ga_mxfp8_bf16_BpreShuffle_256x256" + ("_splitK" if l2 else "")
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=100 + M + l2, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    check(got, expect(qa, sa, qb, sb, l2), "decode path M=%d N=%d K=%d gdz=%d" %
+          (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
+@pytest.mark.parametrize("M", [1, 40])
+def test_decode_path_plain_b_and_epilogue(dev, M):
+    """Row-major B and alpha/beta through the small-M path."""
+    N, K = 512, 1024
+    cfg = cfg_named("ga_mxfp8_bf16_noBpreShuffle_256x256")
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=7 + M)
+    rng = np.random.default_rng(M)
+    c_in = oracle.to_bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0, alpha=0.5, beta=2.0, c_in=c_in)
+    acc = oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, 0, 1.0)
+    want_f = (np.float32(0.5) * acc).astype(np.float32) + np.float32(2.0) * \
+        oracle.bf16_bits_to_f32(c_in)
+    check(got, oracle.to_bf16_bits(want_f.astype(np.float32)), "decode plain-B alpha/beta M=%d" % M,
+          0.5 * oracle.mx_absdot(qa, sa, qb, sb))
