@@ -9,8 +9,13 @@ C ABI (select_kernel -> make_launch -> fill_args -> kernel launch). Inputs are
 synthetic: N(0,1) values scaled by 2^u per 1x32 block (u uniform in [-4, 4]),
 quantised on the GPU by the library's MX quantiser (scale rule floor(log2(amax/448))).
 
-Also measured (reported in "decode"): the decode GEMM M=16, N=28672, K=8192
-with weights from N(0, 0.02), rotating 3 weight sets (> 256 MB Infinity Cache).
+Also measured (reported in "decode"): the decode GEMMs M=16, N=28672, K=8192
+and M=16, N=8192, K=28672 with weights from N(0, 0.02), rotating 3 weight sets
+(> 256 MB Infinity Cache), at the reference driver's default log2_k_split=0.
+
+"mfma_ceiling" is the rate of the scaled-MFMA instruction alone (no memory
+traffic) on the 8192^3 problem's own A operand bytes, with the shader clock it
+ran at (libgcnasm_probe.so): the power-limited ceiling for this data.
 
 The CPU baseline is the reference's own CPU GEMM (asm_f4gemm/f4gemm_ref.hpp
 reference_gemm, compiled in place into oracle/_ref) on a bounded row sample of
@@ -36,6 +41,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first copy 512 MiB device-to-device twice (counter calibration "
+                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     return ap.parse_args()
 
 
@@ -74,19 +82,80 @@ def time_gemm(torch, f4gemm, a, bs, M, N, K, steps, warmup, log2_k_split=0, name
     for i in range(warmup):
         kern.launch(args[i % len(args)], ld.gdx, ld.gdy, ld.gdz, stream=stream, workspace=ws)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    # timed region: back-to-back launches bracketed by two events on the
+    # launch stream; average launch duration = region / steps
+    e_start, e_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e_start.record(stream)
     for i in range(steps):
-        ev[i][0].record(stream)
         kern.launch(args[i % len(args)], ld.gdx, ld.gdy, ld.gdz, stream=stream, workspace=ws)
-        ev[i][1].record(stream)
+    e_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    avg = e_start.elapsed_time(e_end) * 1e3 / steps
+    # spread: a few launches timed one by one
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(min(steps, 10))]
+    for i, (e0, e1) in enumerate(ev):
+        e0.record(stream)
+        kern.launch(args[i % len(args)], ld.gdx, ld.gdy, ld.gdz, stream=stream, workspace=ws)
+        e1.record(stream)
+    torch.cuda.synchronize()
     per = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)  # us per launch
-    avg = sum(per) / len(per)
     return dict(cfg=cfg, ld=ld, wall_s=wall, avg_us=avg, best_us=per[0],
                 median_us=per[len(per) // 2])
+
+
+def mfma_ceiling(torch, codes):
+    """Sustained scaled-MFMA rate on `codes` (uint8 tensor) and the clock."""
+    import ctypes
+    path = os.path.join(ROOT, "gcnasm_amd", "libgcnasm_probe.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    blocks, iters = 1024, 4096
+    sink = torch.zeros(blocks, device="cuda:0")
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    nbytes = min(codes.numel(), 1 << 26)
+
+    def go():
+        st = lib.ga_probe_mfma(ctypes.c_void_p(codes.data_ptr()), ctypes.c_uint32(nbytes), iters,
+                               blocks, ctypes.c_void_p(sink.data_ptr()),
+                               ctypes.c_void_p(clk.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+        assert st == 0, "probe launch failed"
+    go()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    go()
+    go()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 2 * 1e-3
+    flops = blocks * 8 * iters * 8 * 2.0 * 16 * 16 * 128
+    c = clk.view(blocks, 2).double()
+    ghz = float((c[:, 0] / (c[:, 1] * 10.0)).mean())
+    return {"value": round(flops / t / 1e12, 1), "unit": "TFLOP/s",
+            "frac_of_peak": round(flops / t / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "clock_ghz": round(ghz, 3),
+            "what": "v_mfma_scale_f32_16x16x128_f8f6f4 only, 8 waves/CU, operands = the "
+                    "8192^3 problem's quantised A bytes"}
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of the 8192^3 kernel from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 512 MiB copy),
+    or None when no summary for this kernel is committed."""
+    path = os.path.join(ROOT, "profiles", "mxfp8_8192_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel:
+        return None
+    return t.get("bytes_per_launch")
 
 
 def cpu_baseline(M, N, K, seconds):
@@ -131,23 +200,41 @@ def main():
     import torch
     from gcnasm_amd import f4gemm, ops
 
+    if args.calib_copy:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     M = N = K = 8192
     a, bs = mx_problem(torch, ops, f4gemm, M, N, K)
     r = time_gemm(torch, f4gemm, a, bs, M, N, K, args.steps, args.warmup)
     flops = 2.0 * M * N * K
     tflops_wall = flops * args.steps / r["wall_s"] / 1e12
     achieved = flops / (r["avg_us"] * 1e-6) / 1e12
+    ceiling = mfma_ceiling(torch, a.codes)
     del a, bs
     torch.cuda.empty_cache()
 
-    # decode, M=16: HBM-bound; rotate weight sets so the Infinity Cache cannot serve them
-    dM, dN, dK = 16, 28672, 8192
-    da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=1)
-    dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30), args.warmup,
-                   log2_k_split=-1)
-    dbytes = dM * dK + dN * dK + (dM + dN) * dK / 32 + 2 * dM * dN
-    dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
-    del da, dbs
+    # decode, M=16: HBM-bound; rotate weight sets so the Infinity Cache cannot
+    # serve them; log2_k_split=0 is the reference driver's default
+    decode = []
+    for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672)):
+        da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=1)
+        dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30), args.warmup,
+                       log2_k_split=0)
+        dbytes = dM * dK + dN * dK + (dM + dN) * dK / 32 + 2 * dM * dN
+        dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
+        decode.append({"workload": "mxfp8_gemm_decode_%dx%dx%d" % (dM, dN, dK),
+                       "value": round(dgbs, 1), "unit": "GB/s", "kernel": dr["cfg"].knl_name,
+                       "grid": [dr["ld"].gdx, dr["ld"].gdy, dr["ld"].gdz],
+                       "kernel_avg_us": round(dr["avg_us"], 2),
+                       "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4),
+                       "algorithmic_bytes": int(dbytes), "weight_sets": 3})
+        del da, dbs
+        torch.cuda.empty_cache()
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
@@ -169,13 +256,10 @@ def main():
                    "kernel_median_us": round(r["median_us"], 2)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                     "traffic": None},
-        "decode": {"workload": "mxfp8_gemm_decode_16x28672x8192", "value": round(dgbs, 1),
-                   "unit": "GB/s", "kernel": dr["cfg"].knl_name,
-                   "grid": [dr["ld"].gdx, dr["ld"].gdy, dr["ld"].gdz],
-                   "kernel_avg_us": round(dr["avg_us"], 2),
-                   "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4),
-                   "algorithmic_bytes": int(dbytes), "weight_sets": 3},
+                     "traffic": measured_traffic(r["cfg"].knl_name)},
+        "decode": decode[0],
+        "decode_other": decode[1:],
+        "mfma_ceiling": ceiling,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)

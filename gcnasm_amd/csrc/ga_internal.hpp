@@ -28,15 +28,16 @@ typedef void (*mx_launch_fn)(const ga_f4gemm_kargs& args, float* ws, int gdx, in
 struct MxKernel {
     ga_tile_config cfg;
     mx_launch_fn launch;
-    bool small_m_stream; // M <= 64 goes to the decode path (launch_mx_decode)
+    int small_m_stream; // M up to this many rows goes to the decode path (launch_mx_decode)
 };
 // 256x256 eight-wave kernels (gemm_mx_pp.hip), preshuffled / plain B.
 void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                       hipStream_t stream);
 void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                         hipStream_t stream);
-// Small-M (decode) path of the 256x256 kernels (gemm_mx_decode.hip): streams
-// B into registers, K slices summed in the workgroup (no workspace).
+// Small-M (decode) path shared by the kernels (gemm_mx_decode.hip): streams B
+// into registers, K slices summed in the workgroup (no workspace). Results
+// equal the tile kernels' (one fp32 chain of 128-K steps per slice).
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz);
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, int num_cu,
                       hipStream_t stream);

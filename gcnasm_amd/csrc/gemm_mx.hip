@@ -304,7 +304,7 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, false}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 32}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
@@ -314,7 +314,7 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
 #define GA_MX_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                 \
     {{256, 256, SPLIT, BPS, "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
-     &FN, true}
+     &FN, 64}
 
 static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
@@ -432,7 +432,7 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
             return fail(GA_ERR_ARG, "gdz=%d does not match log2_k_split=%d", gdz, L);
     }
     hipStream_t s = (hipStream_t)stream;
-    if (k.small_m_stream && mx_decode_applies(*args, gdz)) {
+    if ((int)args->M <= k.small_m_stream && mx_decode_applies(*args, gdz)) {
         // few rows: stream B, K slices summed inside the kernel (no workspace)
         int num_cu = 0;
         ga_status st = device_cu_count(&num_cu);
