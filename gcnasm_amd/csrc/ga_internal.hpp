@@ -44,6 +44,9 @@ void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, int num_cu
 
 // Compute units of the current device (queried once per device).
 ga_status device_cu_count(int* num_cu);
+// 256x256 eight-wave fp32-scaled FP8 GEMM (gemm_bs_pp.hip); mode 0 = block
+// scale GROUP_N 128, 1 = GROUP_N 1, 2 = per-tensor.
+void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStream_t stream);
 int mx_registry_count();  // manifest rows
 int mx_registry_total();  // manifest rows + kernels reachable only by name
 const MxKernel* mx_registry_get(int idx);

@@ -13,10 +13,11 @@
 // through the buffer range check; a partial last N group of 128 is fine).
 // C is fp32 (the reference's output type) or bf16.
 //
-// Same machinery as the MX kernel: 4 waves, BM x BN tile, K step 128,
-// A and B staged with buffer_load ... lds into the MFMA-order LDS image,
+// Up to 64 rows (this file): 4 waves, 64x256 tile, K step 128, A and B
+// staged with buffer_load ... lds into the MFMA-order LDS image,
 // v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales (127) and the
-// operands swapped so a lane owns 4 consecutive N of one C row.
+// operands swapped so a lane owns 4 consecutive N of one C row. More rows go
+// to the 256x256 eight-wave kernel of gemm_bs_pp.hip.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
 
@@ -271,15 +272,14 @@ static ga_status launch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
 template <int MODE, int OUT>
 static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
 {
-    // The block-scale modes keep the fp32 accumulators in VGPRs (VALU fmaf
-    // per group), so their largest tile is 128x128; the per-tensor mode
-    // accumulates inside the MFMA and takes 256x128.
-    const long long tiles = (long long)((ka.m + 255) / 256) * ((ka.n + 127) / 128) * ka.batch;
-    if (MODE == BS_TENSOR && tiles >= 128)
-        return launch_bs<BsCfg<256, 128, 2, 2, MODE, OUT>>(ka, stream);
-    if (ka.m <= 64)
-        return launch_bs<BsCfg<64, 256, 1, 4, MODE, OUT>>(ka, stream);
-    return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
+    // More than 64 rows: the 256x256 eight-wave kernel (gemm_bs_pp.hip).
+    // Up to 64 rows: this file's 64x256 four-wave tile.
+    if (ka.m > 64) {
+        launch_bs_pp(ka, MODE, OUT, stream);
+        GA_HIP_CHECK(hipGetLastError());
+        return GA_OK;
+    }
+    return launch_bs<BsCfg<64, 256, 1, 4, MODE, OUT>>(ka, stream);
 }
 
 static ga_status check_kargs(const ga_opus_gemm_kargs* ka)

@@ -1,0 +1,431 @@
+// gemm_bs_pp.hip -- 256x256 FP8 GEMM with fp32 scales behind the
+// opus_gemm_kargs ABI: DeepSeek block scale (1x128 activations, 128x128 or
+// 1x128 weights) and per-tensor scale, fp32 or bf16 C, batched.
+//
+//   block-scale: C[b,m,n] = sum_g P_g[m,n] * SFA[g, m] * SFB(g, n),
+//                acc = fmaf(P_g, SFA*SFB, acc) per 128-K group g in K order
+//   per-tensor:  C = (sfa[0] * sfb[0]) * sum_k A*B, one fp32 chain
+//
+// The structure is the MXFP8 256x256 kernel's (gemm_mx_pp.hip, ga_pp.hpp):
+// eight waves in two groups one barrier apart, K step 128 in four phases of
+// one 128x128 quadrant, A and B row-major in swizzled LDS rows, two K-step
+// slots refilled half tile by half tile. Differences:
+//  * the MFMA runs with unit E8M0 scales into a zeroed temporary (8 tiles x
+//    4 VGPRs); the fp32 scaling of quadrant k is folded into its accumulator
+//    in the NEXT MFMA slot, tile by tile just before the MFMA that reuses the
+//    tile's temporary, so the VALU work issues between MFMAs: s = SFA[m] *
+//    SFB (GROUP_N 1: per column), then four fmaf per tile and lane;
+//  * per K group the scales travel with the operands: SFA[g, m0..m0+255]
+//    (1 KB, copied by waves 0-3, permuted so a lane's four rows are one
+//    16-byte LDS read) and SFB (waves 4-7: the tile's two 128-column blocks,
+//    or its 256 columns for GROUP_N 1) into a ring of four 2 KB slots;
+//  * per-tensor: the MFMA accumulates across K and the epilogue applies
+//    sfa[0] * sfb[0].
+#include "ga_device.hpp"
+#include "ga_internal.hpp"
+#include "ga_pp.hpp"
+
+namespace ga {
+namespace {
+
+using namespace pp;
+
+enum { PS_GROUP128 = 0, PS_GROUP1 = 1, PS_TENSOR = 2 };
+
+constexpr int kSSlot = 2048; // SFA (1 KB) + SFB (1 KB) of one K group
+constexpr int kSRing = 4;    // scale slots: group s in slot s % 4
+constexpr int kSBase = kOperandBytes;
+constexpr int kLdsBs = kSBase + kSRing * kSSlot;
+static_assert(kLdsBs <= 160 * 1024, "LDS budget");
+constexpr int kBsGroupM = 4;
+
+struct BsLoad {
+    __amdgpu_buffer_rsrc_t ra, rb, rs; // rs: SFA (waves 0-3) or SFB (waves 4-7)
+    uint32_t va, vb, vs;               // per-lane offsets (half 0, copy 0, K group 0)
+    uint32_t a_hstep, b_hstep;         // bytes between copies 0 and 1 (64 rows)
+    uint32_t s_kstep;                  // scale bytes per K group
+};
+
+__device__ __forceinline__ void issue_a(const BsLoad& L, char* smem, int h, int t, int wave)
+{
+    char* dst = smem + kARegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
+    const uint32_t o = (uint32_t)h * 2 * L.a_hstep + (uint32_t)t * 128;
+    lds_load16(L.ra, (lds_void*)dst, L.va + uni(o), 0);
+    lds_load16(L.ra, (lds_void*)(dst + 8192), L.va + uni(o + L.a_hstep), 0);
+}
+
+__device__ __forceinline__ void issue_b(const BsLoad& L, char* smem, int h, int t, int wave)
+{
+    char* dst = smem + kBRegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
+    const uint32_t o = (uint32_t)h * 2 * L.b_hstep + (uint32_t)t * 128;
+    lds_load16(L.rb, (lds_void*)dst, L.vb + uni(o), 0);
+    lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb + uni(o + L.b_hstep), 0);
+}
+
+// Scales of K group t into ring slot `ring`: one 4-byte copy per lane.
+__device__ __forceinline__ void issue_s(const BsLoad& L, char* smem, int t, int ring, int wave)
+{
+    char* dst = smem + kSBase + ring * kSSlot + wave * 256;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4,
+                                             L.vs + uni((uint32_t)t * L.s_kstep), 0, 0, 0);
+}
+
+struct BsRead {
+    const char* a0;
+    const char* a1;
+    const char* b0;
+    const char* b1;
+    const char* sa; // this lane's four rows of group grp
+    const char* sb; // GROUP_N 1: this lane's four columns of tile 0 (simd block)
+};
+
+template <int H>
+__device__ __forceinline__ void read_a(const BsRead& rb, int slot, v8i (&a)[4])
+{
+    const int off = kARegion + slot * kOpSlot + H * kHalf;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        a[i] = lds_frag(rb.a0 + off + i * 2048, rb.a1 + off + i * 2048);
+}
+
+template <int H>
+__device__ __forceinline__ void read_b(const BsRead& rb, int slot, v8i (&b)[2])
+{
+    const int off = slot * kOpSlot + H * kHalf; // base includes the B region
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+        b[t] = lds_frag(rb.b0 + off + t * 2048, rb.b1 + off + t * 2048);
+}
+
+// Scales of quadrant (HM, HN) of the K group in ring slot `ring`: this
+// lane's four SFA rows and its SFB value(s).
+struct ScaleVals {
+    v4f sa;
+    v4f sb0, sb1; // GROUP_N 1: columns of tiles 0 and 1; GROUP_N 128: sb0[0]
+};
+
+template <int MODE, int HM, int HN>
+__device__ __forceinline__ ScaleVals read_scales(const BsRead& rb, int ring)
+{
+    ScaleVals v;
+    if constexpr (MODE != PS_TENSOR) {
+        v.sa = *(const v4f*)(rb.sa + ring * kSSlot + HM * 2 * 256);
+        if constexpr (MODE == PS_GROUP128) {
+            v.sb0[0] = *(const float*)(rb.sb + ring * kSSlot + HN * 4);
+        } else {
+            const char* sbp = rb.sb + ring * kSSlot + HN * 128 * 4;
+            v.sb0 = *(const v4f*)sbp;
+            v.sb1 = *(const v4f*)(sbp + 64);
+        }
+    }
+    return v;
+}
+
+// acc += p * (SFA * SFB), the product rounded to fp32 first.
+template <int MODE>
+__device__ __forceinline__ void apply_scales(const ScaleVals& v, v4f (&acc)[4][2],
+                                             const v4f (&p)[4][2])
+{
+    if constexpr (MODE == PS_GROUP128) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float s = v.sa[i] * v.sb0[0];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][t][j] = __builtin_fmaf(p[i][t][j], s, acc[i][t][j]);
+        }
+    } else if constexpr (MODE == PS_GROUP1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc[i][0][j] = __builtin_fmaf(p[i][0][j], v.sa[i] * v.sb0[j], acc[i][0][j]);
+                acc[i][1][j] = __builtin_fmaf(p[i][1][j], v.sa[i] * v.sb1[j], acc[i][1][j]);
+            }
+    }
+}
+
+// MFMA slot: the quadrant's 8 MFMAs (4 A tiles x 2 B tiles of one 128-K
+// group; unit E8M0 scales). For the block-scale modes each MFMA writes a
+// zeroed temporary p[i][t], and just before it the previous quadrant's
+// p[i][t] is folded into its accumulator (acc += p * SFA*SFB): the VALU work
+// of a tile issues while the MFMA pipe runs the previous tile's MFMA.
+template <int MODE, bool APPLY>
+__device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], v4f (&p)[4][2], const v8i (&a)[4],
+                                             const v8i (&b)[2], v4f (&acc_prev)[4][2],
+                                             const ScaleVals& sv)
+{
+    __builtin_amdgcn_s_setprio(1);
+    static_for<4>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        static_for<2>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            if constexpr (MODE == PS_TENSOR) {
+                acc[i][t] = mfma_mx16<0, 0>(b[t], a[i], acc[i][t], 127, 127);
+            } else {
+                // keep the order fold(tile) -> MFMA(tile), tile by tile
+                if constexpr (APPLY)
+                    __builtin_amdgcn_sched_group_barrier(
+                        0x2, MODE == PS_GROUP128 ? (t == 0 ? 5 : 4) : 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x8, 1, 0);
+                if constexpr (APPLY) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float s = MODE == PS_GROUP128 ? sv.sa[i] * sv.sb0[0]
+                                                            : sv.sa[i] * (t ? sv.sb1[j] : sv.sb0[j]);
+                        acc_prev[i][t][j] = __builtin_fmaf(p[i][t][j], s, acc_prev[i][t][j]);
+                    }
+                }
+                p[i][t] = mfma_mx16<0, 0>(b[t], a[i], (v4f){0.f, 0.f, 0.f, 0.f}, 127, 127);
+            }
+        });
+    });
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// Memory slot: the copy, the scales of the quadrant the next MFMA slot
+// folds in, then the operand read (the MFMA slot's first fold waits only for
+// the scale reads, each MFMA only for its own operand), then the phase
+// boundary.
+#define BS_MEM_SLOT(HMP, HNP, RING, COPIES, READS, WAITN)                                    \
+    {                                                                                        \
+        COPIES;                                                                              \
+        sv = read_scales<MODE, HMP, HNP>(rb, RING);                                          \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        READS;                                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        phase_sync<WAITN>();                                                                 \
+    }
+
+template <int MODE, int OUT>
+__global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
+void bs_pp_kernel(ga_opus_gemm_kargs ka)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[kLdsBs];
+    constexpr int S = MODE == PS_TENSOR ? 0 : 1; // scale copies per wave per K group
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, simd = wave & 3;
+    const int M = ka.m, N = ka.n, K = ka.k;
+    int tile_m, tile_n;
+    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, kBsGroupM, tile_m, tile_n);
+    const int m0 = tile_m * 256, n0 = tile_n * 256;
+    const int b = blockIdx.z;
+    const int nsteps = K / 128;
+
+    v4f acc[4][4][2];
+    v4f p[4][2]; // MFMA results of the last quadrant, scaled in the next memory slot
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+                acc[q][i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    BsLoad L;
+    {
+        int crow, ckc;
+        copy_lane(wave, lane, crow, ckc);
+        const char* pa = (const char*)ka.ptr_a + (size_t)b * ka.stride_a_batch +
+                         (size_t)m0 * ka.stride_a;
+        const char* pb = (const char*)ka.ptr_b + (size_t)b * ka.stride_b_batch +
+                         (size_t)n0 * ka.stride_b;
+        const long long abytes = (long long)(M - m0) * ka.stride_a;
+        const long long bbytes = (long long)(N - n0) * ka.stride_b;
+        L.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+        L.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+        L.va = (uint32_t)crow * ka.stride_a + ckc * 16;
+        L.vb = (uint32_t)crow * ka.stride_b + ckc * 16;
+        L.a_hstep = 64 * (uint32_t)ka.stride_a;
+        L.b_hstep = 64 * (uint32_t)ka.stride_b;
+        L.vs = 0;
+        L.s_kstep = 0;
+        if constexpr (MODE != PS_TENSOR) {
+            const int ngroups = K / 128;
+            if (wave < 4) {
+                // SFA [K/128, M]: LDS position w*64 + l holds row
+                // w*64 + (l%4)*16 + l/4 (rows past M clamp to M-1)
+                const float* sfa = (const float*)ka.ptr_sfa + (size_t)b * ka.stride_sfa_batch;
+                L.rs = make_rsrc(sfa, (uint32_t)ngroups * ka.stride_sfa * 4);
+                const int row = min(m0 + wave * 64 + (lane & 3) * 16 + (lane >> 2), M - 1);
+                L.vs = (uint32_t)row * 4;
+                L.s_kstep = (uint32_t)ka.stride_sfa * 4;
+            } else {
+                const float* sfb = (const float*)ka.ptr_sfb + (size_t)b * ka.stride_sfb_batch;
+                const int pos = (wave - 4) * 64 + lane;
+                if (MODE == PS_GROUP128) {
+                    // SFB [ceil(N/128), K/128]: positions 0 and 1 hold the
+                    // tile's two 128-column blocks
+                    const int nblk = (N + 127) / 128;
+                    L.rs = make_rsrc(sfb, (uint32_t)nblk * ka.stride_sfb * 4);
+                    const int nb = min(n0 / 128 + (pos & 1), nblk - 1);
+                    L.vs = (uint32_t)nb * ka.stride_sfb * 4;
+                    L.s_kstep = 4;
+                } else {
+                    // SFB [K/128, N]: position c holds column n0 + c
+                    L.rs = make_rsrc(sfb, (uint32_t)ngroups * ka.stride_sfb * 4);
+                    const int col = min(n0 + pos, N - 1);
+                    L.vs = (uint32_t)col * 4;
+                    L.s_kstep = (uint32_t)ka.stride_sfb * 4;
+                }
+            }
+        }
+    }
+
+    BsRead rb;
+    {
+        uint32_t o, o64;
+        operand_lane(lane, o, o64);
+        rb.a0 = smem + grp * 64 * 128 + o;
+        rb.a1 = smem + grp * 64 * 128 + o64;
+        rb.b0 = smem + kBRegion + simd * 32 * 128 + o;
+        rb.b1 = smem + kBRegion + simd * 32 * 128 + o64;
+        rb.sa = smem + kSBase + grp * 256 + (lane & 15) * 16;
+        rb.sb = smem + kSBase + 1024 +
+                (MODE == PS_GROUP1 ? (simd * 32 + (lane >> 4) * 4) * 4 : 0);
+    }
+
+    v8i fa[4], fb0[2], fb1[2];
+
+    // Prologue: copies in steady-state order (B0+S, A0, B1, A1 of group 0;
+    // B0+S, A0, B1 of group 1), then the B0 read of the phase before step 0.
+    issue_b(L, smem, 0, 0, wave);
+    if (S)
+        issue_s(L, smem, 0, 0, wave);
+    issue_a(L, smem, 0, 0, wave);
+    issue_b(L, smem, 1, 0, wave);
+    issue_a(L, smem, 1, 0, wave);
+    issue_b(L, smem, 0, 1, wave);
+    if (S)
+        issue_s(L, smem, 1, 1, wave);
+    issue_a(L, smem, 0, 1, wave);
+    issue_b(L, smem, 1, 1, wave);
+    phase_sync<12 + S>(); // B0 (+ scales) of group 0
+    read_b<0>(rb, 0, fb0);
+    phase_sync<10 + S>(); // A0 of group 0
+    if (grp == 1)
+        slot_sync(); // second group runs one barrier behind
+
+    // K group s (LDS slot s & 1, scale ring slot r0). A memory slot first
+    // applies the scales of the quadrant the previous MFMA slot produced,
+    // then issues its copy, then its operand read, then waits:
+    //   phase  read      copy            quadrant   younger copies
+    //   1      A0(s)     A1(s+1)         00         10 + S
+    //   2      B1(s)     B0+S(s+2)       01         10 + 2S
+    //   3      A1(s)     A0(s+2)         10         10 + S
+    //   4      B0(s+1)   B1(s+2)         11         10 + S
+    // The loop's first quadrant has nothing to fold in: peel it.
+    // Scale ring slot of group s: s % 4. The copy of group s+2 (phase 2 of
+    // group s) overwrites group s-2's slot, last read for the fold in phase 1
+    // of group s-1.
+    ScaleVals sv;
+    for (int s = 0; s < nsteps; s++) {
+        const int slot = s & 1;
+        const int r0 = s & 3, r2 = (s + 2) & 3, rprev = (s - 1) & 3;
+        // phase 1 (folds in quadrant 11 of the previous group)
+        BS_MEM_SLOT(1, 1, rprev, issue_a(L, smem, 1, s + 1, wave), read_a<0>(rb, slot, fa),
+                    10 + S);
+        if (s > 0)
+            mma_quadrant<MODE, true>(acc[0], p, fa, fb0, acc[3], sv);
+        else
+            mma_quadrant<MODE, false>(acc[0], p, fa, fb0, acc[3], sv);
+        slot_sync();
+        // phase 2
+        BS_MEM_SLOT(0, 0, r0,
+                    issue_b(L, smem, 0, s + 2, wave); if (S) issue_s(L, smem, s + 2, r2, wave),
+                    read_b<1>(rb, slot, fb1), 10 + 2 * S);
+        mma_quadrant<MODE, true>(acc[1], p, fa, fb1, acc[0], sv);
+        slot_sync();
+        // phase 3
+        BS_MEM_SLOT(0, 1, r0, issue_a(L, smem, 0, s + 2, wave), read_a<1>(rb, slot, fa), 10 + S);
+        mma_quadrant<MODE, true>(acc[2], p, fa, fb0, acc[1], sv);
+        slot_sync();
+        // phase 4
+        BS_MEM_SLOT(1, 0, r0, issue_b(L, smem, 1, s + 2, wave), read_b<0>(rb, slot ^ 1, fb0),
+                    10 + S);
+        mma_quadrant<MODE, true>(acc[3], p, fa, fb1, acc[2], sv);
+        slot_sync();
+    }
+    if (grp == 0)
+        slot_sync(); // matches the second group's extra barrier
+    {
+        const ScaleVals last = read_scales<MODE, 1, 1>(rb, (nsteps - 1) & 3);
+        apply_scales<MODE>(last, acc[3], p);
+    }
+    wait_vmcnt<0>(); // copies past K land before exit
+
+    // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile.
+    float tscale = 1.0f;
+    if constexpr (MODE == PS_TENSOR)
+        tscale = ((const float*)ka.ptr_sfa)[0] * ((const float*)ka.ptr_sfb)[0];
+    char* pc = (char*)ka.ptr_c + (size_t)b * ka.stride_c_batch * (OUT == GA_DTYPE_F32 ? 4 : 2);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = m0 + (q >> 1) * 128 + grp * 64 + i * 16 + (lane & 15);
+            if (m >= M)
+                continue;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int n = n0 + (q & 1) * 128 + simd * 32 + t * 16 + (lane >> 4) * 4;
+                if (n >= N)
+                    continue;
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    v[j] = MODE == PS_TENSOR ? acc[q][i][t][j] * tscale : acc[q][i][t][j];
+                const size_t off = (size_t)m * ka.stride_c + n;
+                const bool full = n + 4 <= N && (ka.stride_c & 3) == 0;
+                if constexpr (OUT == GA_DTYPE_F32) {
+                    float* o = (float*)pc + off;
+                    if (full)
+                        *(v4f*)o = (v4f){v[0], v[1], v[2], v[3]};
+                    else
+                        for (int j = 0; j < 4 && n + j < N; j++)
+                            o[j] = v[j];
+                } else {
+                    uint16_t* o = (uint16_t*)pc + off;
+                    if (full) {
+                        uint2 pk;
+                        pk.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                        pk.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                        *(uint2*)o = pk;
+                    } else {
+                        for (int j = 0; j < 4 && n + j < N; j++)
+                            o[j] = f32_to_bf16(v[j]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int MODE, int OUT>
+void launch_bs_pp_t(const ga_opus_gemm_kargs& ka, hipStream_t stream)
+{
+    const int tn = (ka.n + 255) / 256, tm = (ka.m + 255) / 256;
+    hipLaunchKernelGGL((bs_pp_kernel<MODE, OUT>), dim3(tn, tm, ka.batch), dim3(kNT), 0, stream, ka);
+}
+
+} // namespace
+
+void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStream_t stream)
+{
+    const bool f32 = out_dtype == GA_DTYPE_F32;
+    if (mode == PS_GROUP128)
+        f32 ? launch_bs_pp_t<PS_GROUP128, GA_DTYPE_F32>(ka, stream)
+            : launch_bs_pp_t<PS_GROUP128, GA_DTYPE_BF16>(ka, stream);
+    else if (mode == PS_GROUP1)
+        f32 ? launch_bs_pp_t<PS_GROUP1, GA_DTYPE_F32>(ka, stream)
+            : launch_bs_pp_t<PS_GROUP1, GA_DTYPE_BF16>(ka, stream);
+    else
+        f32 ? launch_bs_pp_t<PS_TENSOR, GA_DTYPE_F32>(ka, stream)
+            : launch_bs_pp_t<PS_TENSOR, GA_DTYPE_BF16>(ka, stream);
+}
+
+} // namespace ga

@@ -37,17 +37,15 @@
 //    operand for the copies (uniform parts added from SGPRs).
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
+#include "ga_pp.hpp"
 
 namespace ga {
 namespace {
 
-constexpr int kNT = 512;
-constexpr int kHalf = 16384;  // 128 rows x 128 K of fp8
-constexpr int kOpSlot = 2 * kHalf;
-constexpr int kARegion = 0;   // A: [slot][half] half tiles
-constexpr int kBRegion = 2 * kOpSlot;
+using namespace pp;
+
 constexpr int kScaleSlot = 16 * 256; // 8 A + 8 B shuffled 32-row scale blocks
-constexpr int kScaleBase = 4 * kOpSlot;
+constexpr int kScaleBase = kOperandBytes;
 constexpr int kLds = kScaleBase + 3 * kScaleSlot;
 static_assert(kLds <= 160 * 1024, "LDS budget");
 constexpr int kPpGroupM = 4;
@@ -60,19 +58,6 @@ struct PpLoad {
     uint32_t b_kstep;      // B bytes per 128-K step
     uint32_t s_blk;        // scale bytes between this wave's two blocks
 };
-
-// Uniform byte offset as an SGPR operand, kept opaque so the per-copy
-// address is formed at the copy (one VGPR base per operand, no hoisted
-// per-copy VGPRs).
-__device__ __forceinline__ uint32_t uni(uint32_t x)
-{
-    return __builtin_amdgcn_readfirstlane(x);
-}
-
-__device__ __forceinline__ void wait_lds_barrier()
-{
-    asm volatile("s_barrier" ::: "memory");
-}
 
 // Copies (2 per wave) of A half tile h of K step t.
 __device__ __forceinline__ void issue_a(const PpLoad& L, char* smem, int h, int t, int wave)
@@ -100,13 +85,6 @@ __device__ __forceinline__ void issue_s(const PpLoad& L, char* smem, int t, int 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4, L.vs + uni(q), 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + 256), 4,
                                              L.vs + uni(q + L.s_blk), 0, 0, 0);
-}
-
-__device__ __forceinline__ v8i lds_frag(const char* p0, const char* p1)
-{
-    v4i x0 = *(const v4i*)p0;
-    v4i x1 = *(const v4i*)p1;
-    return (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 }
 
 // Per-lane LDS read bases. Swizzled row-major operand: lane 16g + r reads
@@ -178,23 +156,6 @@ __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4]
     __builtin_amdgcn_s_setprio(0);
 }
 
-// Phase boundary: own copies waited for (count = copies issued after the
-// ones the next phase reads), then the workgroup barrier.
-template <int N>
-__device__ __forceinline__ void phase_sync()
-{
-    wait_vmcnt<N>();
-    wait_lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-__device__ __forceinline__ void slot_sync()
-{
-    __builtin_amdgcn_sched_barrier(0);
-    wait_lds_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 template <bool BPS>
 __global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
 void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
@@ -233,8 +194,8 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         // + lane*16 = row c*64 + wave*8 + lane/8, slot lane%8, which holds K
         // chunk slot ^ ((row >> 1) & 7); the chunk does not depend on c or
         // the half (64 and 128 rows keep (row >> 1) & 7).
-        const int crow = wave * 8 + (lane >> 3);
-        const int ckc = (lane & 7) ^ ((crow >> 1) & 7);
+        int crow, ckc;
+        copy_lane(wave, lane, crow, ckc);
         {
             const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
             long long abytes = (long long)(M - m0) * lda;
@@ -276,16 +237,16 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
 
         ReadBase rb;
         {
-            const uint32_t r = lane & 15, g = lane >> 4;
-            const uint32_t o = r * 128 + ((g ^ ((r >> 1) & 7)) * 16);
+            uint32_t o, o64;
+            operand_lane(lane, o, o64);
             rb.a0 = smem + grp * 64 * 128 + o;
-            rb.a1 = smem + grp * 64 * 128 + (o ^ 64u);
+            rb.a1 = smem + grp * 64 * 128 + o64;
             if (BPS) {
                 rb.b0 = smem + kBRegion + simd * 32 * 128 + lane * 16;
                 rb.b1 = rb.b0 + 1024;
             } else {
                 rb.b0 = smem + kBRegion + simd * 32 * 128 + o;
-                rb.b1 = smem + kBRegion + simd * 32 * 128 + (o ^ 64u);
+                rb.b1 = smem + kBRegion + simd * 32 * 128 + o64;
             }
             rb.sa = smem + kScaleBase + grp * 2 * 256 + lane * 4;
             rb.sb = smem + kScaleBase + (8 + simd) * 256 + lane * 4;

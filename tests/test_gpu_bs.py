@@ -48,7 +48,8 @@ def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
 
 @pytest.mark.parametrize("group_n", [128, 1])
 @pytest.mark.parametrize("shape", [(256, 512, 256), (384, 2112, 1024), (96, 1000, 512),
-                                   (33, 7168, 512), (1, 256, 384)])
+                                   (33, 7168, 512), (1, 256, 384), (520, 784, 1152),
+                                   (65, 300, 640)])
 def test_blockscale(dev, group_n, shape):
     M, N, K = shape
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + N, group_n=group_n)
@@ -82,7 +83,8 @@ def test_blockscale_batched(dev):
         assert st["bad"] == 0, b
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 512), (200, 1040, 1024), (1, 512, 256)])
+@pytest.mark.parametrize("shape", [(256, 256, 512), (200, 1040, 1024), (1, 512, 256),
+                                   (600, 1000, 768)])
 def test_per_tensor(dev, shape):
     M, N, K = shape
     xa = oracle.randn(M * K, 11).reshape(M, K)
