@@ -13,6 +13,11 @@ Also measured (reported in "decode"): the decode GEMMs M=16, N=28672, K=8192
 and M=16, N=8192, K=28672 with weights from N(0, 0.02), rotating 3 weight sets
 (> 256 MB Infinity Cache), at the reference driver's default log2_k_split=0.
 
+"blockscale" times the DeepSeek-style GEMM (1x128 activation / 128x128 weight
+fp32 scales, fp32 C, opus_gemm kargs) at 8192^3 next to the reference's own
+published number for it (opus_gemm/block_scale_gemm/README.md:114), and the
+per-tensor fp8_gemm at 8192^3 (bf16 C).
+
 "mfma_ceiling" is the rate of the scaled-MFMA instruction alone (no memory
 traffic) on the 8192^3 problem's own A operand bytes, with the shader clock it
 ran at (libgcnasm_probe.so): the power-limited ceiling for this data.
@@ -143,6 +148,54 @@ def mfma_ceiling(torch, codes):
                     "8192^3 problem's quantised A bytes"}
 
 
+REF_BLOCKSCALE_8192_TFLOPS = 2710.24  # opus_gemm/block_scale_gemm/README.md:114 (MI355X)
+
+
+def time_call(torch, fn, steps, warmup):
+    """Average duration (us) of back-to-back calls between two events."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
+    """DeepSeek block-scale (fp32 C) and per-tensor (bf16 C) GEMMs at 8192^3."""
+    n = 8192
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(2)
+    xa = torch.randn((n, n), device="cuda:0", generator=g)
+    xb = torch.randn((n, n), device="cuda:0", generator=g)
+    qa, sfa = ops.quant_fp8_1x128(xa)
+    qb, sfb = ops.quant_fp8_128x128(xb)
+    c = torch.empty((n, n), dtype=torch.float32, device="cuda:0")
+    us = time_call(torch, lambda: opus_gemm.blockscale_gemm(qa, qb, sfa, sfb, c), steps, warmup)
+    del qa, qb, sfa, sfb, c
+    flops = 2.0 * n ** 3
+    bs = {"workload": "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out",
+          "value": round(flops / us / 1e6, 1), "unit": "TFLOP/s", "kernel_avg_us": round(us, 2),
+          "frac_fp8_peak": round(flops / us / 1e6 / FP8_PEAK_TFLOPS, 4),
+          "reference_published": REF_BLOCKSCALE_8192_TFLOPS,
+          "vs_reference": round(flops / us / 1e6 / REF_BLOCKSCALE_8192_TFLOPS, 4)}
+    qa, sa = ops.quant_fp8_per_tensor(xa)
+    qb, sb = ops.quant_fp8_per_tensor(xb)
+    c = torch.empty((n, n), dtype=torch.bfloat16, device="cuda:0")
+    us = time_call(torch, lambda: opus_gemm.per_tensor_gemm(qa, qb, sa, sb, c), steps, warmup)
+    pt = {"workload": "fp8_per_tensor_8192x8192x8192_bf16out",
+          "value": round(flops / us / 1e6, 1), "unit": "TFLOP/s", "kernel_avg_us": round(us, 2),
+          "frac_fp8_peak": round(flops / us / 1e6 / FP8_PEAK_TFLOPS, 4)}
+    del xa, xb, qa, qb, c
+    torch.cuda.empty_cache()
+    return bs, pt
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of the 8192^3 kernel from the committed rocprofv3
     counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 512 MiB copy),
@@ -198,7 +251,7 @@ def main():
               "design is described in DESIGN.md" % args.gpus, file=sys.stderr)
         sys.exit(2)
     import torch
-    from gcnasm_amd import f4gemm, ops
+    from gcnasm_amd import f4gemm, opus_gemm, ops
 
     if args.calib_copy:
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -236,6 +289,8 @@ def main():
         del da, dbs
         torch.cuda.empty_cache()
 
+    blockscale, per_tensor = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
+
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
         "value": round(tflops_wall, 2),
@@ -260,6 +315,8 @@ def main():
         "decode": decode[0],
         "decode_other": decode[1:],
         "mfma_ceiling": ceiling,
+        "blockscale": blockscale,
+        "per_tensor": per_tensor,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)

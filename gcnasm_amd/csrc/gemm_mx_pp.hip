@@ -23,6 +23,9 @@
 //    step two ahead once both groups have read it, so its copy has six phases
 //    to land; every phase ends with a counted vmcnt wait on the copy the next
 //    phase reads.
+//  * A shuffled scale dword covers 256 K, a pair of K steps, so a ring slot
+//    holds one pair (8 A then 8 B 32-row blocks) and each step copies half of
+//    the pair two ahead: one 4-byte-per-lane copy per wave per step.
 //  * Row-major operands (A, and B without preshuffle) sit in LDS as 128-byte
 //    rows, 16-byte K chunk c of row r at slot c ^ ((r >> 1) & 7). Each copy
 //    instruction then reads 8 whole 128-byte rows (whole cache lines; a copy
@@ -51,12 +54,12 @@ static_assert(kLds <= 160 * 1024, "LDS budget");
 constexpr int kPpGroupM = 4;
 
 struct PpLoad {
-    __amdgpu_buffer_rsrc_t ra, rb, rs;
-    uint32_t va, vb, vs;   // per-lane copy offsets (half 0, copy 0, first K step)
+    __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
+    uint32_t va, vb;       // per-lane copy offsets (half 0, copy 0, first K step)
+    uint32_t vsa, vsb;     // per-lane offsets of this wave's A / B scale block
     uint32_t a_hstep;      // A bytes between copies 0 and 1 of a half (64 rows)
     uint32_t b_hstep;      // same for B
     uint32_t b_kstep;      // B bytes per 128-K step
-    uint32_t s_blk;        // scale bytes between this wave's two blocks
 };
 
 // Copies (2 per wave) of A half tile h of K step t.
@@ -76,15 +79,16 @@ __device__ __forceinline__ void issue_b(const PpLoad& L, char* smem, int h, int 
     lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb + uni(o + L.b_hstep), 0);
 }
 
-// Scales of K step t into ring slot `ring`: wave w copies blocks 2w, 2w+1
-// (blocks 0-7: A rows, 8-15: B rows). A shuffled dword covers 256 K.
-__device__ __forceinline__ void issue_s(const PpLoad& L, char* smem, int t, int ring, int wave)
+// Half `half` (0: A rows, 1: B rows) of the scales of K-step pair `pair`
+// into ring slot `ring`: wave w copies 32-row block w of that operand.
+__device__ __forceinline__ void issue_s(const PpLoad& L, char* smem, int pair, int half,
+                                        int ring, int wave)
 {
-    char* dst = smem + kScaleBase + ring * kScaleSlot + wave * 512;
-    const uint32_t q = (uint32_t)(t >> 1) * 256;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4, L.vs + uni(q), 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + 256), 4,
-                                             L.vs + uni(q + L.s_blk), 0, 0, 0);
+    char* dst = smem + kScaleBase + ring * kScaleSlot + half * 2048 + wave * 256;
+    const uint32_t q = (uint32_t)pair * 256;
+    const __amdgpu_buffer_rsrc_t r = half ? L.rsb : L.rsa;
+    const uint32_t v = half ? L.vsb : L.vsa;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 4, v + uni(q), 0, 0, 0);
 }
 
 // Per-lane LDS read bases. Swizzled row-major operand: lane 16g + r reads
@@ -105,8 +109,10 @@ __device__ __forceinline__ void read_a(const ReadBase& rb, int slot, v8i (&a)[4]
 {
     const int off = kARegion + slot * kOpSlot + H * kHalf;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
         a[i] = lds_frag(rb.a0 + off + i * 2048, rb.a1 + off + i * 2048);
+        __builtin_amdgcn_sched_barrier(0); // issue in MFMA order: counted waits
+    }
 }
 
 // B fragment of slot `slot`, half H: columns H*128 + simd*32 + [0, 32).
@@ -119,22 +125,23 @@ __device__ __forceinline__ void read_b(const ReadBase& rb, int slot, v8i (&b)[2]
         b[t] = lds_frag(rb.b0 + off + t * 2048, rb.b1 + off + t * 2048);
 }
 
-// Scale dwords of ring slot `ring`. Byte 2*d4 + d1 of a dword holds 128-K
-// half d4 (the step's parity) of 16-row half d1; the shift by `sh` (16 for
-// odd steps) moves this step's half to bytes 0-1.
+// Scales of ring slot `ring`. Byte 2*d4 + d1 of a shuffled dword holds
+// 128-K half d4 (the step's parity) of 16-row half d1: a 16-bit read at byte
+// offset `hb` = 2 * parity lands this step's two bytes in bits 0-15, straight
+// into the MFMA scale operand (no ALU op between the read and the MFMA).
 template <int H>
-__device__ __forceinline__ void read_sa(const ReadBase& rb, int ring, uint32_t sh,
+__device__ __forceinline__ void read_sa(const ReadBase& rb, int ring, uint32_t hb,
                                         uint32_t (&s)[2])
 {
-    const char* p = rb.sa + ring * kScaleSlot + H * 4 * 256;
-    s[0] = *(const uint32_t*)p >> sh;
-    s[1] = *(const uint32_t*)(p + 256) >> sh;
+    const char* p = rb.sa + ring * kScaleSlot + H * 4 * 256 + hb;
+    s[0] = *(const uint16_t*)p;
+    s[1] = *(const uint16_t*)(p + 256);
 }
 
 template <int H>
-__device__ __forceinline__ uint32_t read_sb(const ReadBase& rb, int ring, uint32_t sh)
+__device__ __forceinline__ uint32_t read_sb(const ReadBase& rb, int ring, uint32_t hb)
 {
-    return *(const uint32_t*)(rb.sb + ring * kScaleSlot + H * 4 * 256) >> sh;
+    return *(const uint16_t*)(rb.sb + ring * kScaleSlot + H * 4 * 256 + hb);
 }
 
 // One quadrant: 4 A tiles x 2 B tiles; the scale byte is 2*P + (16-row
@@ -222,17 +229,14 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
                 L.vb = (uint32_t)crow * ldb + ckc * 16 + (uint32_t)kb;
             }
             // scales: shuffled layout, 256-byte block per (32 rows, 256 K);
-            // wave w copies blocks 2w, 2w+1 of the tile's 16 (A 0-7, B 8-15)
-            const bool sb = wave >= 4;
-            const uint32_t sn = sb ? args.stride_ScaleB0 : args.stride_ScaleA0;
-            const int rows = sb ? N : M;
-            const int base = sb ? n0 : m0;
-            L.rs = make_rsrc(sb ? args.ptr_ScaleB : args.ptr_ScaleA,
-                             (uint32_t)((rows + 31) / 32 * 32) * sn);
-            const int blk = (wave & 3) * 2;
-            L.vs = ((uint32_t)((base + blk * 32) / 32) * (sn / 8) + (uint32_t)(kb / 256)) * 256 +
-                   lane * 4;
-            L.s_blk = (sn / 8) * 256;
+            // wave w copies block w of the tile's 8 A and 8 B blocks
+            const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
+            L.rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)((M + 31) / 32 * 32) * sna);
+            L.rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)((N + 31) / 32 * 32) * snb);
+            L.vsa = ((uint32_t)(m0 / 32 + wave) * (sna / 8) + (uint32_t)(kb / 256)) * 256 +
+                    lane * 4;
+            L.vsb = ((uint32_t)(n0 / 32 + wave) * (snb / 8) + (uint32_t)(kb / 256)) * 256 +
+                    lane * 4;
         }
 
         ReadBase rb;
@@ -258,21 +262,27 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         uint32_t sa[2], sb0, sb1;
 
         // Prologue: the copies a steady pipeline would have issued before
-        // step 0, in the same order (B0+S, A0, B1, A1 of step 0; B0+S, A0, B1
-        // of step 1), then the read of the phase before step 0 (B0).
+        // step 0, in the same order (scales of pair 0; B0 + A scales of pair
+        // 1, A0, B1, A1 of step 0; B0 + B scales of pair 1, A0, B1 of step 1),
+        // then the read of the phase before step 0 (B0).
+        issue_s(L, smem, 0, 0, 0, wave);
+        issue_s(L, smem, 0, 1, 0, wave);
         issue_b(L, smem, 0, 0, wave);
-        issue_s(L, smem, 0, 0, wave);
+        issue_s(L, smem, 1, 0, 1, wave);
         issue_a(L, smem, 0, 0, wave);
         issue_b(L, smem, 1, 0, wave);
         issue_a(L, smem, 1, 0, wave);
         issue_b(L, smem, 0, 1, wave);
-        issue_s(L, smem, 1, 1, wave);
+        issue_s(L, smem, 1, 1, 1, wave);
         issue_a(L, smem, 0, 1, wave);
         issue_b(L, smem, 1, 1, wave);
-        phase_sync<14>(); // B0 + scales of step 0
+        phase_sync<14>(); // B0 of step 0 and the scales of pair 0
         read_b<0>(rb, 0, fb0);
-        sb0 = read_sb<0>(rb, 0, 0);
-        phase_sync<12>(); // A0 of step 0
+        phase_sync<11>(); // A0 of step 0
+        // Retire pending scalar loads (epilogue arguments) here: with one in
+        // flight the compiler cannot count LDS reads inside the loop and
+        // falls back to full waits.
+        wait_lgkmcnt0();
         if (grp == 1)
             slot_sync(); // second group runs one barrier behind
 
@@ -281,43 +291,47 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         // finished reading) before its LDS reads, then waits for the copy
         // the next phase reads:
         //   phase  read        copy           quadrant   younger copies
-        //   1      A0(s)       A1(s+1)        00         12
-        //   2      B1(s)       B0+S(s+2)      01         14
+        //   1      A0(s)       A1(s+1)        00         11
+        //   2      B1(s)       B0(s+2), S     01         12
         //   3      A1(s)       A0(s+2)        10         12
-        //   4      B0(s+1)     B1(s+2)        11         12
-        int r0 = 0; // scale ring slot of step s
+        //   4      B0(s+1)     B1(s+2)        11         11
+        // S is half P of the scales of pair (s >> 1) + 2 (ring slot r2, the
+        // slot of pair (s >> 1) - 1, whose last read was in step s - 1 or
+        // earlier); the scales a phase reads were copied at least two steps
+        // before the operand copy it waits for, so that wait covers them.
+        int r0 = 0; // scale ring slot of pair s >> 1
         for (int s = 0; s < nsteps; s++) {
             const int P = s & 1;
-            const uint32_t sh = (uint32_t)P * 16, sh1 = (uint32_t)(P ^ 1) * 16;
-            const int r1 = r0 == 2 ? 0 : r0 + 1;
-            const int r2 = r1 == 2 ? 0 : r1 + 1;
+            const uint32_t hb = (uint32_t)P * 2;
+            const int r1 = P ? (r0 == 2 ? 0 : r0 + 1) : r0; // pair of step s + 1
+            const int r2 = r0 == 0 ? 2 : r0 - 1;              // (r0 + 2) % 3
             // phase 1
             issue_a(L, smem, 1, s + 1, wave);
-            read_sa<0>(rb, r0, sh, sa);
+            read_sa<0>(rb, r0, hb, sa);
+            sb0 = read_sb<0>(rb, r0, hb);
             read_a<0>(rb, P, fa);
-            phase_sync<12>();
+            phase_sync<11>();
             mma_quadrant<0>(acc[0], fa, fb0, sa, sb0);
             slot_sync();
             // phase 2
             issue_b(L, smem, 0, s + 2, wave);
-            issue_s(L, smem, s + 2, r2, wave);
-            sb1 = read_sb<1>(rb, r0, sh);
+            issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
+            sb1 = read_sb<1>(rb, r0, hb);
             read_b<1>(rb, P, fb1);
-            phase_sync<14>();
+            phase_sync<12>();
             mma_quadrant<0>(acc[1], fa, fb1, sa, sb1);
             slot_sync();
             // phase 3
             issue_a(L, smem, 0, s + 2, wave);
-            read_sa<1>(rb, r0, sh, sa);
+            read_sa<1>(rb, r0, hb, sa);
             read_a<1>(rb, P, fa);
             phase_sync<12>();
             mma_quadrant<0>(acc[2], fa, fb0, sa, sb0);
             slot_sync();
             // phase 4
             issue_b(L, smem, 1, s + 2, wave);
-            sb0 = read_sb<0>(rb, r1, sh1);
             read_b<0>(rb, P ^ 1, fb0);
-            phase_sync<12>();
+            phase_sync<11>();
             mma_quadrant<0>(acc[3], fa, fb1, sa, sb1);
             slot_sync();
             r0 = r1;
