@@ -192,15 +192,15 @@ __device__ __forceinline__ int mx_scale_exp(float amax, int rule)
     return e < -127 ? -127 : (e > 127 ? 127 : e);
 }
 
-// Workgroup (x, y) -> (tile_m, tile_n). Workgroup ids are dispatched
-// round-robin over the 8 XCDs; the remap gives each XCD a contiguous range of
-// tiles, swept column by column inside groups of `group_m` M-tiles so the
-// workgroups resident on one XCD share A and B panels in its L2.
-__device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int group_m, int& tm,
-                                         int& tn)
+// Linear tile id -> (tile_m, tile_n) on a gdx x gdy tile grid. Workgroup ids
+// are dispatched round-robin over the 8 XCDs; the remap gives each XCD a
+// contiguous range of tiles, swept column by column inside groups of
+// `group_m` M-tiles so the workgroups resident on one XCD share A and B
+// panels in its L2.
+__device__ __forceinline__ void map_tile_lin(int lin, int gdx, int gdy, int group_m, int& tm,
+                                             int& tn)
 {
     const int total = gdx * gdy;
-    int lin = by * gdx + bx;
     const int full = (total / 8) * 8;
     if (lin < full)
         lin = (lin % 8) * (total / 8) + lin / 8;
@@ -211,6 +211,12 @@ __device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int g
     const int r = lin - g * per_group;
     tm = first_m + r % gsize;
     tn = r / gsize;
+}
+
+__device__ __forceinline__ void map_tile(int bx, int by, int gdx, int gdy, int group_m, int& tm,
+                                         int& tn)
+{
+    map_tile_lin(by * gdx + bx, gdx, gdy, group_m, tm, tn);
 }
 
 } // namespace ga

@@ -26,6 +26,14 @@ constexpr int kOperandBytes = 4 * kOpSlot;
 // is formed at the copy (one VGPR base per operand, no hoisted per-copy VGPRs).
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
+template <class T>
+__device__ __forceinline__ T* uni_ptr(T* p)
+{
+    const uint64_t u = (uint64_t)(uintptr_t)p;
+    const uint64_t lo = uni((uint32_t)u), hi = uni((uint32_t)(u >> 32));
+    return (T*)(uintptr_t)((hi << 32) | lo);
+}
+
 __device__ __forceinline__ void wait_lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // Phase boundary: own copies waited for (N = copies issued after the ones
@@ -36,6 +44,35 @@ __device__ __forceinline__ void phase_sync()
     wait_vmcnt<N>();
     wait_lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// Staged epilogue: a 256x256 bf16 tile goes through LDS as rows of 528 bytes
+// (512 + 16: the 16 rows x 2 lanes of one ds_write_b64 half-wave start on
+// distinct bank quads), so the global stores write whole 512-byte rows
+// instead of 16 rows x 32 bytes per instruction.
+constexpr int kStagePitch = 528;
+constexpr int kStageBytes = 256 * kStagePitch;
+
+__device__ __forceinline__ void stage_put(char* smem, int row, int col, uint32_t lo, uint32_t hi)
+{
+    uint2 v;
+    v.x = lo;
+    v.y = hi;
+    *(uint2*)(smem + row * kStagePitch + col * 2) = v;
+}
+
+// Wave w stores rows 32w .. 32w+31 of the staged tile, two rows (64 lanes x
+// 16 B) per instruction, to dst (the tile's first element, row stride ldd).
+__device__ __forceinline__ void stage_store(const char* smem, uint16_t* dst, int ldd, int wave,
+                                            int lane)
+{
+    const int col = (lane & 31) * 8;
+#pragma unroll
+    for (int it = 0; it < 16; it++) {
+        const int row = wave * 32 + it * 2 + (lane >> 5);
+        const v4i d = *(const v4i*)(smem + row * kStagePitch + col * 2);
+        *(v4i*)(dst + (size_t)row * ldd + col) = d;
+    }
 }
 
 __device__ __forceinline__ void slot_sync()

@@ -163,18 +163,34 @@ __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4]
     __builtin_amdgcn_s_setprio(0);
 }
 
-template <bool BPS>
-__global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
-void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
-{
-    __shared__ __attribute__((aligned(1024))) char smem[kLds];
+// The kernel-argument fields a tile uses (names as in ga_f4gemm_kargs), read
+// once at kernel entry and made wave-uniform: the compiler fetches this large
+// by-value argument with vector loads, and every address derived from a VGPR
+// copy would need its own VGPRs and readfirstlanes in the K loop.
+struct PpArgs {
+    const void* ptr_A;
+    const void* ptr_B;
+    const void* ptr_ScaleA;
+    const void* ptr_ScaleB;
+    const void* ptr_C;
+    void* ptr_D;
+    float alpha, beta;
+    uint32_t M, N, K, stride_A0, stride_B0, stride_ScaleA0, stride_ScaleB0, stride_C0;
+    int log2_k_split;
+};
 
+// One 256x256 output tile (K slice blockIdx.z): prologue, K loop, epilogue.
+// On return every LDS read of the tile is complete (the last barrier is
+// after the last read); copies of steps past the slice may still be landing,
+// each into the LDS bytes its own wave writes first in the next tile.
+template <bool BPS>
+__device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ ws,
+                                        char* smem, int tile_m, int tile_n)
+{
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2, simd = wave & 3;
     const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
-    int tile_m, tile_n;
-    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, kPpGroupM, tile_m, tile_n);
     const int m0 = tile_m * 256, n0 = tile_n * 256;
 
     const int z = blockIdx.z, gdz = gridDim.z;
@@ -338,7 +354,6 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         }
         if (grp == 0)
             slot_sync(); // matches the second group's extra barrier
-        wait_vmcnt<0>(); // copies of steps past the slice land before exit
     }
 
     // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile. The library is
@@ -346,6 +361,32 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
     const int ldd = (int)args.stride_C0;
     const float alpha = args.alpha, beta = args.beta;
     const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+    // Whole interior tiles without C go through LDS (whole-row stores).
+    const bool staged = gdz == 1 && !use_c && m0 + 256 <= M && n0 + 256 <= N &&
+                        (ldd & 7) == 0 && ((uintptr_t)args.ptr_D & 15) == 0;
+    if (staged) {
+        static_assert(kStageBytes <= kLds, "staging fits in LDS");
+        wait_vmcnt<0>();   // copies of steps past the slice have landed
+        wait_lds_barrier(); // ... in every wave, and every operand read is done
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const v4f v = acc[q][i][t];
+                    const uint32_t lo = (uint32_t)f32_to_bf16(alpha * v[0]) |
+                                        ((uint32_t)f32_to_bf16(alpha * v[1]) << 16);
+                    const uint32_t hi = (uint32_t)f32_to_bf16(alpha * v[2]) |
+                                        ((uint32_t)f32_to_bf16(alpha * v[3]) << 16);
+                    stage_put(smem, (q >> 1) * 128 + grp * 64 + i * 16 + (lane & 15),
+                              (q & 1) * 128 + simd * 32 + t * 16 + (lane >> 4) * 4, lo, hi);
+                }
+        barrier_lds();
+        stage_store(smem, (uint16_t*)args.ptr_D + (size_t)m0 * ldd + n0, ldd, wave, lane);
+        barrier_lds(); // staged rows read before the LDS takes the next tile's copies
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
 #pragma unroll
@@ -380,18 +421,72 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
     }
 }
 
+// Persistent grid: workgroup b computes tiles b, b + gridDim.x, ... of the
+// tiles_x x tiles_y tile grid (gridDim.x a multiple of 8, or all tiles in one
+// pass, so each workgroup stays on the XCD map_tile assigns its tiles to).
+// The epilogue stores of one tile drain while the next tile's first copies
+// are in flight, instead of behind a workgroup exit and a new launch.
+template <bool BPS>
+__global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
+void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws, int tiles_x, int tiles_y)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[kLds];
+    PpArgs a;
+    a.ptr_A = uni_ptr(args.ptr_A);
+    a.ptr_B = uni_ptr(args.ptr_B);
+    a.ptr_ScaleA = uni_ptr(args.ptr_ScaleA);
+    a.ptr_ScaleB = uni_ptr(args.ptr_ScaleB);
+    a.ptr_C = uni_ptr(args.ptr_C);
+    a.ptr_D = uni_ptr(args.ptr_D);
+    a.alpha = args.alpha; // epilogue VALU operands: may stay in VGPRs
+    a.beta = args.beta;
+    a.M = uni(args.M);
+    a.N = uni(args.N);
+    a.K = uni(args.K);
+    a.stride_A0 = uni(args.stride_A0);
+    a.stride_B0 = uni(args.stride_B0);
+    a.stride_ScaleA0 = uni(args.stride_ScaleA0);
+    a.stride_ScaleB0 = uni(args.stride_ScaleB0);
+    a.stride_C0 = uni(args.stride_C0);
+    a.log2_k_split = (int)uni((uint32_t)args.log2_k_split);
+    const int ntiles = tiles_x * tiles_y;
+    for (int lin = blockIdx.x; lin < ntiles; lin += gridDim.x) {
+        int tile_m, tile_n;
+        map_tile_lin(lin, tiles_x, tiles_y, kPpGroupM, tile_m, tile_n);
+        pp_tile<BPS>(a, ws, smem, tile_m, tile_n);
+    }
+    wait_vmcnt<0>(); // copies of steps past the last slice land before exit
+}
+
+} // namespace
+
+namespace {
+
+// Workgroups per K slice: one per CU (rounded down to a multiple of 8) when
+// the tiles outnumber the CUs, else one per tile.
+int pp_grid(int tiles)
+{
+    int cu = 0;
+    if (device_cu_count(&cu) != 0 || cu < 8)
+        return tiles;
+    const int g = cu / 8 * 8;
+    return tiles > g ? g : tiles;
+}
+
 } // namespace
 
 void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                       hipStream_t stream)
 {
-    hipLaunchKernelGGL(mx_pp_kernel<true>, dim3(gdx, gdy, gdz), dim3(kNT), 0, stream, args, ws);
+    hipLaunchKernelGGL(mx_pp_kernel<true>, dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT), 0, stream,
+                       args, ws, gdx, gdy);
 }
 
 void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                         hipStream_t stream)
 {
-    hipLaunchKernelGGL(mx_pp_kernel<false>, dim3(gdx, gdy, gdz), dim3(kNT), 0, stream, args, ws);
+    hipLaunchKernelGGL(mx_pp_kernel<false>, dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT), 0, stream,
+                       args, ws, gdx, gdy);
 }
 
 } // namespace ga
