@@ -150,6 +150,9 @@ SIGNATURES = {
     "ga_manifest_count": (_i, []),
     "ga_manifest_get": (_i, [_i, ctypes.POINTER(TileConfig)]),
     "ga_manifest_csv": (_i, [ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]),
+    "ga_manifest_fp4_count": (_i, []),
+    "ga_manifest_fp4_get": (_i, [_i, ctypes.POINTER(TileConfig)]),
+    "ga_manifest_fp4_csv": (_i, [ctypes.c_char_p, _sz, ctypes.POINTER(_sz)]),
     "ga_load_configs": (_i, [ctypes.c_char_p, ctypes.POINTER(TileConfig), _i,
                              ctypes.POINTER(_i)]),
     "ga_select_kernel": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(TileConfig), _i,
@@ -164,6 +167,7 @@ SIGNATURES = {
     "ga_shuffle_weight_16x16_device": (_i, [_vp, _vp, _i, _i, _vp]),
     "ga_shuffle_scale_device": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
     "ga_quant_mxfp8": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
+    "ga_quant_mxfp4": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
     "ga_quant_fp8_1x128": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ga_quant_fp8_128x128": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ga_quant_fp8_per_tensor": (_i, [_vp, _i, _sz, _vp, _vp, _vp, _vp]),
@@ -171,6 +175,8 @@ SIGNATURES = {
     "ga_kernel_workspace_bytes": (_sz, [_i, ctypes.POINTER(LaunchDesc), _i, _i]),
     "ga_kernel_launch": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _sz, _vp]),
     "ga_mxfp8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
+                           ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
+    "ga_mxfp4_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
                            ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
     "ga_gemm_a8w8_blockscale": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _i, _vp]),
     "ga_fp8_gemm_per_tensor": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _vp]),

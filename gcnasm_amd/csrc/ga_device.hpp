@@ -113,6 +113,24 @@ __device__ __forceinline__ v4f mfma_mx16(v8i a, v8i b, v4f c, int sa, int sb)
                                                             sb);
 }
 
+// Same with fp4 (e2m1) operands: lane l = 16*g + r holds row r, K
+// [32g, 32g+32) in its first 16 bytes (two elements per byte, low nibble
+// first); the last 16 bytes of the operand are not read. Scales and output as
+// above.
+template <int OPSEL_A, int OPSEL_B>
+__device__ __forceinline__ v4f mfma_mx16_fp4(v8i a, v8i b, v4f c, int sa, int sb)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 4, OPSEL_A, sa, OPSEL_B,
+                                                            sb);
+}
+
+// The last 16 bytes of a fragment moved to its first 16 (the fp4 operand
+// of the second 128-K half).
+__device__ __forceinline__ v8i hi16(v8i x)
+{
+    return (v8i){x[4], x[5], x[6], x[7], 0, 0, 0, 0};
+}
+
 // fp32 -> bf16 round to nearest even (quiet NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16(float x)
 {
@@ -171,9 +189,11 @@ __device__ __forceinline__ void log2_parts(float a, int& E, uint32_t& frac)
     }
 }
 
-// E8M0 exponent of an MX block (rule 0: floor(log2(amax/448)), 1: ceil,
-// 2: OCP floor(log2 amax) - 8). Zero block -> -127.
-__device__ __forceinline__ int mx_scale_exp(float amax, int rule)
+// E8M0 exponent of an MX block whose element format has largest value
+// (1 + FRAC/2^23) * 2^EMAX: rule 0: floor(log2(amax/max)), 1: ceil, 2: OCP
+// floor(log2 amax) - EMAX. Zero block -> -127.
+template <uint32_t FRAC, int EMAX>
+__device__ __forceinline__ int mx_scale_exp_t(float amax, int rule)
 {
     if (!(amax > 0.0f))
         return -127;
@@ -184,12 +204,37 @@ __device__ __forceinline__ int mx_scale_exp(float amax, int rule)
     log2_parts(amax, E, f);
     int e;
     if (rule == 0)
-        e = (f >= 0x600000u) ? E - 8 : E - 9;
+        e = (f >= FRAC) ? E - EMAX : E - EMAX - 1;
     else if (rule == 1)
-        e = (f <= 0x600000u) ? E - 8 : E - 7;
+        e = (f <= FRAC) ? E - EMAX : E - EMAX + 1;
     else
-        e = E - 8;
+        e = E - EMAX;
     return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+// E4M3: 448 = 1.75 * 2^8.
+__device__ __forceinline__ int mx_scale_exp(float amax, int rule)
+{
+    return mx_scale_exp_t<0x600000u, 8>(amax, rule);
+}
+
+// E2M1: 6 = 1.5 * 2^2.
+__device__ __forceinline__ int mx4_scale_exp(float amax, int rule)
+{
+    return mx_scale_exp_t<0x400000u, 2>(amax, rule);
+}
+
+// OCP E2M1 encode (MXFP4 element; values 0, .5, 1, 1.5, 2, 3, 4, 6, sign in
+// bit 3): round to nearest, ties to the even code, saturate to +-6. E2M1 has
+// no NaN: NaN gives a zero with its sign bit.
+__device__ __forceinline__ uint32_t e2m1_encode(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    const float a = __uint_as_float(u & 0x7FFFFFFFu);
+    const uint32_t c = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) +
+                       (uint32_t)(a >= 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) +
+                       (uint32_t)(a > 5.0f);
+    return ((u >> 28) & 8u) | c;
 }
 
 // Linear tile id -> (tile_m, tile_n) on a gdx x gdy tile grid. Workgroup ids

@@ -22,19 +22,25 @@ ga_status hip_fail(hipError_t e, const char* what);
             return ::ga::hip_fail(e_, #call);               \
     } while (0)
 
-// One compiled MXFP8 kernel: the manifest row plus its launcher.
+// One compiled MX kernel: the manifest row plus its launcher.
 typedef void (*mx_launch_fn)(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy,
                              int gdz, hipStream_t stream);
 struct MxKernel {
     ga_tile_config cfg;
     mx_launch_fn launch;
     int small_m_stream; // M up to this many rows goes to the decode path (launch_mx_decode)
+    int elem_bits;      // 8: E4M3 operands, 4: e2m1 packed two per byte
 };
 // 256x256 eight-wave kernels (gemm_mx_pp.hip), preshuffled / plain B.
 void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                       hipStream_t stream);
 void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                         hipStream_t stream);
+// The same tile for MXFP4 operands (e2m1, packed two per byte).
+void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                       hipStream_t stream);
+void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                         hipStream_t stream);
 // Small-M (decode) path shared by the kernels (gemm_mx_decode.hip): streams B
 // into registers, K slices summed in the workgroup (no workspace). Results
 // equal the tile kernels' (one fp32 chain of 128-K steps per slice).
@@ -47,9 +53,11 @@ ga_status device_cu_count(int* num_cu);
 // 256x256 eight-wave fp32-scaled FP8 GEMM (gemm_bs_pp.hip); mode 0 = block
 // scale GROUP_N 128, 1 = GROUP_N 1, 2 = per-tensor.
 void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStream_t stream);
-int mx_registry_count();  // manifest rows
-int mx_registry_total();  // manifest rows + kernels reachable only by name
+int mx_registry_count();  // MXFP8 manifest rows (registry entries [0, count))
+int mx_registry_total();  // every registry entry (manifests + kernels reachable by name)
 const MxKernel* mx_registry_get(int idx);
+int mx4_registry_first(); // MXFP4 manifest rows: entries [first, first + count)
+int mx4_registry_count();
 
 // Library-owned per-device fp32 workspace, grown on demand.
 ga_status default_workspace(size_t bytes, void** ptr);

@@ -304,7 +304,7 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 32}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 32, 8}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
@@ -314,7 +314,12 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
 #define GA_MX_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                 \
     {{256, 256, SPLIT, BPS, "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
-     &FN, 64}
+     &FN, 64, 8}
+// MXFP4 (the reference's f4gemm_bf16_per1x32Fp4 kernels): e2m1 operands.
+#define GA_MX4_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                \
+    {{256, 256, SPLIT, BPS, "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
+      "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
+     &FN, 0, 4}
 
 static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
@@ -335,10 +340,18 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
     // not in the manifest: the 4-wave 256x256 tile (two stages)
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
+    // the MXFP4 manifest
+    GA_MX4_PP_ENTRY(1, 0, "", launch_mx4_pp_bps),
+    GA_MX4_PP_ENTRY(1, 1, "_splitK", launch_mx4_pp_bps),
+    GA_MX4_PP_ENTRY(0, 0, "", launch_mx4_pp_nobps),
 };
 constexpr int kManifestCount = 16;
+constexpr int kMx4First = 17;
+constexpr int kMx4Count = 3;
 
 int mx_registry_count() { return kManifestCount; }
+int mx4_registry_first() { return kMx4First; }
+int mx4_registry_count() { return kMx4Count; }
 int mx_registry_total() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
 const MxKernel* mx_registry_get(int idx) { return &g_mx_kernels[idx]; }
 
@@ -405,16 +418,22 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
     if (M <= 0 || N <= 0 || K <= 0 || !args->ptr_A || !args->ptr_B || !args->ptr_D ||
         !args->ptr_ScaleA || !args->ptr_ScaleB)
         return fail(GA_ERR_ARG, "kernel_launch: null pointer or empty shape");
-    if (K % 128 != 0)
-        return fail(GA_ERR_SHAPE, "K must be a multiple of 128 (got %d)", K);
+    // K granule: one K step (128 E4M3 / 256 e2m1 elements: 128 bytes per row),
+    // the reference driver's K % 256 for MXFP4 (asm_f4gemm/README.md:43).
+    const int kstep = k.elem_bits == 4 ? 256 : 128;
+    const uint32_t row_align = k.elem_bits == 4 ? 32 : 16; // 16-byte rows, in elements
+    if (K % kstep != 0)
+        return fail(GA_ERR_SHAPE, "K must be a multiple of %d (got %d)", kstep, K);
     if (N % 16 != 0)
         return fail(GA_ERR_SHAPE, "N must be a multiple of 16 (got %d)", N);
     if (args->stride_C0 % 4 != 0 || args->stride_C0 < (uint32_t)N)
         return fail(GA_ERR_SHAPE, "stride_C0 must be >= N and a multiple of 4 (got %u)",
                     args->stride_C0);
-    if (args->stride_A0 % 16 != 0 || args->stride_A0 < (uint32_t)K ||
-        (!k.cfg.bpreshuffle && (args->stride_B0 % 16 != 0 || args->stride_B0 < (uint32_t)K)))
-        return fail(GA_ERR_SHAPE, "A/B row strides must be >= K and multiples of 16");
+    if (args->stride_A0 % row_align != 0 || args->stride_A0 < (uint32_t)K ||
+        (!k.cfg.bpreshuffle &&
+         (args->stride_B0 % row_align != 0 || args->stride_B0 < (uint32_t)K)))
+        return fail(GA_ERR_SHAPE, "A/B row strides (elements) must be >= K and multiples of %u",
+                    row_align);
     if (args->stride_ScaleA0 < (uint32_t)(K / 32) || args->stride_ScaleA0 % 8 ||
         args->stride_ScaleB0 < (uint32_t)(K / 32) || args->stride_ScaleB0 % 8)
         return fail(GA_ERR_SHAPE, "scale strides must be the padded column count "
@@ -506,6 +525,45 @@ ga_status ga_mxfp8_gemm(void* d_D, const void* d_A, const void* d_B, const void*
         return st;
     ga_mx_shape sh;
     st = ga_mx_shape_init(M, N, K, 8, &sh);
+    if (st != GA_OK)
+        return st;
+    ga_f4gemm_kargs args;
+    ga_fill_args(&args, d_D, nullptr, (void*)d_A, (void*)d_B, (void*)d_ScaleA, (void*)d_ScaleB,
+                 M, N, K, stride_D0, sh.scale_cols, sh.scale_cols, 1.0f, 0.0f, ld.log2_k_split);
+    if (chosen)
+        *chosen = idx;
+    if (ld_out)
+        *ld_out = ld;
+    return ga_kernel_launch(idx, &args, ld.gdx, ld.gdy, ld.gdz, workspace, workspace_bytes,
+                            stream);
+}
+
+ga_status ga_mxfp4_gemm(void* d_D, const void* d_A, const void* d_B, const void* d_ScaleA,
+                        const void* d_ScaleB, int M, int N, int K, int stride_D0,
+                        int bpreshuffle, int log2_k_split, int num_cu, void* workspace,
+                        size_t workspace_bytes, int* chosen, ga_launch_desc* ld_out,
+                        void* stream)
+{
+    if (num_cu <= 0) {
+        ga_status st = ga_device_num_cu(&num_cu);
+        if (st != GA_OK)
+            return st;
+    }
+    ga_tile_config table[kMx4Count];
+    for (int i = 0; i < kMx4Count; i++)
+        table[i] = g_mx_kernels[kMx4First + i].cfg;
+    int row = -1, l2 = 0;
+    ga_status st = ga_select_kernel(M, N, K, num_cu, log2_k_split, bpreshuffle, table, kMx4Count,
+                                    &row, &l2);
+    if (st != GA_OK)
+        return st;
+    const int idx = kMx4First + row;
+    ga_launch_desc ld;
+    st = ga_make_launch(&g_mx_kernels[idx].cfg, M, N, K, l2, &ld);
+    if (st != GA_OK)
+        return st;
+    ga_mx_shape sh;
+    st = ga_mx_shape_init(M, N, K, 4, &sh);
     if (st != GA_OK)
         return st;
     ga_f4gemm_kargs args;

@@ -79,8 +79,9 @@ __device__ __forceinline__ void issue_b(const PpLoad& L, char* smem, int h, int 
     lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb + uni(o + L.b_hstep), 0);
 }
 
-// Half `half` (0: A rows, 1: B rows) of the scales of K-step pair `pair`
-// into ring slot `ring`: wave w copies 32-row block w of that operand.
+// Half `half` (0: A rows, 1: B rows) of the shuffled scales of 256-K block
+// `pair` (an MXFP8 step pair, one MXFP4 step) into ring slot `ring`: wave w
+// copies 32-row block w of that operand.
 __device__ __forceinline__ void issue_s(const PpLoad& L, char* smem, int pair, int half,
                                         int ring, int wave)
 {
@@ -129,24 +130,37 @@ __device__ __forceinline__ void read_b(const ReadBase& rb, int slot, v8i (&b)[2]
 // 128-K half d4 (the step's parity) of 16-row half d1: a 16-bit read at byte
 // offset `hb` = 2 * parity lands this step's two bytes in bits 0-15, straight
 // into the MFMA scale operand (no ALU op between the read and the MFMA).
-template <int H>
+// MXFP4 steps are 256 K: the whole dword (both 128-K halves) is read.
+template <int H, bool FP4>
 __device__ __forceinline__ void read_sa(const ReadBase& rb, int ring, uint32_t hb,
                                         uint32_t (&s)[2])
 {
     const char* p = rb.sa + ring * kScaleSlot + H * 4 * 256 + hb;
-    s[0] = *(const uint16_t*)p;
-    s[1] = *(const uint16_t*)(p + 256);
+    if constexpr (FP4) {
+        s[0] = *(const uint32_t*)p;
+        s[1] = *(const uint32_t*)(p + 256);
+    } else {
+        s[0] = *(const uint16_t*)p;
+        s[1] = *(const uint16_t*)(p + 256);
+    }
 }
 
-template <int H>
+template <int H, bool FP4>
 __device__ __forceinline__ uint32_t read_sb(const ReadBase& rb, int ring, uint32_t hb)
 {
-    return *(const uint16_t*)(rb.sb + ring * kScaleSlot + H * 4 * 256 + hb);
+    const char* p = rb.sb + ring * kScaleSlot + H * 4 * 256 + hb;
+    if constexpr (FP4)
+        return *(const uint32_t*)p;
+    else
+        return *(const uint16_t*)p;
 }
 
-// One quadrant: 4 A tiles x 2 B tiles; the scale byte is 2*P + (16-row
-// half inside the 32-row scale block).
-template <int P>
+// One quadrant: 4 A tiles x 2 B tiles; the scale byte is 2*(128-K half) +
+// (16-row half inside the 32-row scale block). MXFP8: one MFMA per tile (the
+// step's 128 K; its half is in bytes 0-1 of the scale operands). MXFP4: the
+// fragment's first 16 bytes per lane are K [0, 128) of the 256-K step and
+// its last 16 bytes K [128, 256): two MFMAs per tile, halves 0 and 1.
+template <bool FP4>
 __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4],
                                              const v8i (&b)[2], const uint32_t (&sa)[2],
                                              uint32_t sb)
@@ -156,8 +170,16 @@ __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4]
         constexpr int i = decltype(I)::value;
         static_for<2>([&](auto T) {
             constexpr int t = decltype(T)::value;
-            acc[i][t] = mfma_mx16<2 * P + (t & 1), 2 * P + (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+            if constexpr (FP4) {
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+                                                            (int)sa[i >> 1]);
+                acc[i][t] = mfma_mx16_fp4<2 + (t & 1), 2 + (i & 1)>(hi16(b[t]), hi16(a[i]),
+                                                                    acc[i][t], (int)sb,
                                                                     (int)sa[i >> 1]);
+            } else {
+                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+                                                        (int)sa[i >> 1]);
+            }
         });
     });
     __builtin_amdgcn_s_setprio(0);
@@ -183,10 +205,17 @@ struct PpArgs {
 // On return every LDS read of the tile is complete (the last barrier is
 // after the last read); copies of steps past the slice may still be landing,
 // each into the LDS bytes its own wave writes first in the next tile.
-template <bool BPS>
+//
+// MXFP4 (FP4): elements are packed two per byte (low nibble first); strides
+// and K count elements. A K step is 256 elements = the same 128 bytes per row
+// as an MXFP8 step, so copies, LDS layout and fragment reads are shared; a
+// step reads one whole shuffled scale dword per 32-row block.
+template <bool BPS, bool FP4>
 __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ ws,
                                         char* smem, int tile_m, int tile_n)
 {
+    constexpr int kEPB = FP4 ? 2 : 1;       // elements per byte
+    constexpr int kStepK = 128 * kEPB;      // elements per K step
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2, simd = wave & 3;
@@ -199,7 +228,8 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
     const int kb = z * kpt;
     const int ke = min(K, kb + kpt);
-    const int nsteps = (ke - kb) / 128;
+    const int nsteps = (ke - kb) / kStepK;
+    const int kbb = kb / kEPB; // byte offset of the slice in a row
 
     v4f acc[4][4][2];
 #pragma unroll
@@ -211,7 +241,8 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
                 acc[q][i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
 
     if (nsteps > 0) {
-        const uint32_t lda = args.stride_A0, ldb = args.stride_B0;
+        const uint32_t lda = args.stride_A0 / kEPB, ldb = args.stride_B0 / kEPB; // bytes
+        const int Kb = K / kEPB;                                                  // bytes
         PpLoad L;
         // Copy c of a row-major half tile writes LDS bytes c*8192 + wave*1024
         // + lane*16 = row c*64 + wave*8 + lane/8, slot lane%8, which holds K
@@ -223,26 +254,26 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
             const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
             long long abytes = (long long)(M - m0) * lda;
             L.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
-            L.va = (uint32_t)crow * lda + ckc * 16 + (uint32_t)kb;
+            L.va = (uint32_t)crow * lda + ckc * 16 + (uint32_t)kbb;
             L.a_hstep = 64 * lda;
             if (BPS) {
-                // preshuffled B: each 16-row group is K*16 contiguous bytes,
-                // [K/16][16 rows][16 B]; one K step is 2 KB of it. Copy c of
+                // preshuffled B: each 16-row group is Kb*16 contiguous bytes,
+                // [Kb/16][16 rows][16 B]; one K step is 2 KB of it. Copy c of
                 // half h: groups h*8 + c*4 + wave/2, bytes (wave&1)*1024 + lane*16.
-                const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
-                long long bbytes = (long long)(N - n0) * K;
+                const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * Kb * 16;
+                long long bbytes = (long long)(N - n0) * Kb;
                 L.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
                 L.b_kstep = 2048;
-                L.b_hstep = 4 * (uint32_t)K * 16;
-                L.vb = (uint32_t)(wave >> 1) * (uint32_t)K * 16 + (wave & 1) * 1024 + lane * 16 +
-                       (uint32_t)kb * 16;
+                L.b_hstep = 4 * (uint32_t)Kb * 16;
+                L.vb = (uint32_t)(wave >> 1) * (uint32_t)Kb * 16 + (wave & 1) * 1024 +
+                       lane * 16 + (uint32_t)kbb * 16;
             } else {
                 const char* pb = (const char*)args.ptr_B + (size_t)n0 * ldb;
                 long long bbytes = (long long)(N - n0) * ldb;
                 L.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
                 L.b_kstep = 128;
                 L.b_hstep = 64 * ldb;
-                L.vb = (uint32_t)crow * ldb + ckc * 16 + (uint32_t)kb;
+                L.vb = (uint32_t)crow * ldb + ckc * 16 + (uint32_t)kbb;
             }
             // scales: shuffled layout, 256-byte block per (32 rows, 256 K);
             // wave w copies block w of the tile's 8 A and 8 B blocks
@@ -278,23 +309,41 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
         uint32_t sa[2], sb0, sb1;
 
         // Prologue: the copies a steady pipeline would have issued before
-        // step 0, in the same order (scales of pair 0; B0 + A scales of pair
-        // 1, A0, B1, A1 of step 0; B0 + B scales of pair 1, A0, B1 of step 1),
-        // then the read of the phase before step 0 (B0).
-        issue_s(L, smem, 0, 0, 0, wave);
-        issue_s(L, smem, 0, 1, 0, wave);
-        issue_b(L, smem, 0, 0, wave);
-        issue_s(L, smem, 1, 0, 1, wave);
-        issue_a(L, smem, 0, 0, wave);
-        issue_b(L, smem, 1, 0, wave);
-        issue_a(L, smem, 1, 0, wave);
-        issue_b(L, smem, 0, 1, wave);
-        issue_s(L, smem, 1, 1, 1, wave);
-        issue_a(L, smem, 0, 1, wave);
-        issue_b(L, smem, 1, 1, wave);
-        phase_sync<14>(); // B0 of step 0 and the scales of pair 0
-        read_b<0>(rb, 0, fb0);
-        phase_sync<11>(); // A0 of step 0
+        // step 0, in the same order, then the read of the phase before step 0
+        // (B0). MXFP8: scales of pair 0; B0 + A scales of pair 1, A0, B1, A1
+        // of step 0; B0 + B scales of pair 1, A0, B1 of step 1. MXFP4: B0 +
+        // scales, A0, B1, A1 of step 0; B0 + scales, A0, B1 of step 1.
+        if constexpr (FP4) {
+            issue_b(L, smem, 0, 0, wave);
+            issue_s(L, smem, 0, 0, 0, wave);
+            issue_s(L, smem, 0, 1, 0, wave);
+            issue_a(L, smem, 0, 0, wave);
+            issue_b(L, smem, 1, 0, wave);
+            issue_a(L, smem, 1, 0, wave);
+            issue_b(L, smem, 0, 1, wave);
+            issue_s(L, smem, 1, 0, 1, wave);
+            issue_s(L, smem, 1, 1, 1, wave);
+            issue_a(L, smem, 0, 1, wave);
+            issue_b(L, smem, 1, 1, wave);
+            phase_sync<16>(); // B0 of step 0
+            read_b<0>(rb, 0, fb0);
+            phase_sync<12>(); // A0 and the scales of step 0
+        } else {
+            issue_s(L, smem, 0, 0, 0, wave);
+            issue_s(L, smem, 0, 1, 0, wave);
+            issue_b(L, smem, 0, 0, wave);
+            issue_s(L, smem, 1, 0, 1, wave);
+            issue_a(L, smem, 0, 0, wave);
+            issue_b(L, smem, 1, 0, wave);
+            issue_a(L, smem, 1, 0, wave);
+            issue_b(L, smem, 0, 1, wave);
+            issue_s(L, smem, 1, 1, 1, wave);
+            issue_a(L, smem, 0, 1, wave);
+            issue_b(L, smem, 1, 1, wave);
+            phase_sync<14>(); // B0 of step 0 and the scales of pair 0
+            read_b<0>(rb, 0, fb0);
+            phase_sync<11>(); // A0 of step 0
+        }
         // Retire pending scalar loads (epilogue arguments) here: with one in
         // flight the compiler cannot count LDS reads inside the loop and
         // falls back to full waits.
@@ -311,44 +360,54 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
         //   2      B1(s)       B0(s+2), S     01         12
         //   3      A1(s)       A0(s+2)        10         12
         //   4      B0(s+1)     B1(s+2)        11         11
-        // S is half P of the scales of pair (s >> 1) + 2 (ring slot r2, the
-        // slot of pair (s >> 1) - 1, whose last read was in step s - 1 or
-        // earlier); the scales a phase reads were copied at least two steps
+        // MXFP8: S is half P of the scales of pair (s >> 1) + 2 (ring slot
+        // r2, the slot of pair (s >> 1) - 1, whose last read was in step s - 1
+        // or earlier); the scales a phase reads were copied at least two steps
         // before the operand copy it waits for, so that wait covers them.
-        int r0 = 0; // scale ring slot of pair s >> 1
+        // MXFP4: S is both halves of the scales of step s + 2 (2 copies, ring
+        // slot (s + 2) % 3 = the slot of step s - 1); they are read from
+        // phase 1 of step s + 2, after the wait for A0(s + 2), which was
+        // issued after them. Younger copies per phase: 12, 14, 14, 12.
+        constexpr int kS = FP4 ? 2 : 1;
+        int r0 = 0; // scale ring slot of step s (MXFP8: of pair s >> 1)
         for (int s = 0; s < nsteps; s++) {
             const int P = s & 1;
-            const uint32_t hb = (uint32_t)P * 2;
-            const int r1 = P ? (r0 == 2 ? 0 : r0 + 1) : r0; // pair of step s + 1
-            const int r2 = r0 == 0 ? 2 : r0 - 1;              // (r0 + 2) % 3
+            const uint32_t hb = FP4 ? 0u : (uint32_t)P * 2;
+            const int r1 = (FP4 || P) ? (r0 == 2 ? 0 : r0 + 1) : r0; // slot of step s + 1
+            const int r2 = r0 == 0 ? 2 : r0 - 1;                       // (r0 + 2) % 3
             // phase 1
             issue_a(L, smem, 1, s + 1, wave);
-            read_sa<0>(rb, r0, hb, sa);
-            sb0 = read_sb<0>(rb, r0, hb);
+            read_sa<0, FP4>(rb, r0, hb, sa);
+            sb0 = read_sb<0, FP4>(rb, r0, hb);
             read_a<0>(rb, P, fa);
-            phase_sync<11>();
-            mma_quadrant<0>(acc[0], fa, fb0, sa, sb0);
+            phase_sync<10 + kS>();
+            mma_quadrant<FP4>(acc[0], fa, fb0, sa, sb0);
             slot_sync();
             // phase 2
             issue_b(L, smem, 0, s + 2, wave);
-            issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
-            sb1 = read_sb<1>(rb, r0, hb);
+            if constexpr (FP4) {
+                issue_s(L, smem, s + 2, 0, r2, wave);
+                issue_s(L, smem, s + 2, 1, r2, wave);
+            } else {
+                issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
+            }
+            sb1 = read_sb<1, FP4>(rb, r0, hb);
             read_b<1>(rb, P, fb1);
-            phase_sync<12>();
-            mma_quadrant<0>(acc[1], fa, fb1, sa, sb1);
+            phase_sync<10 + 2 * kS>();
+            mma_quadrant<FP4>(acc[1], fa, fb1, sa, sb1);
             slot_sync();
             // phase 3
             issue_a(L, smem, 0, s + 2, wave);
-            read_sa<1>(rb, r0, hb, sa);
+            read_sa<1, FP4>(rb, r0, hb, sa);
             read_a<1>(rb, P, fa);
-            phase_sync<12>();
-            mma_quadrant<0>(acc[2], fa, fb0, sa, sb0);
+            phase_sync<10 + 2 * kS>();
+            mma_quadrant<FP4>(acc[2], fa, fb0, sa, sb0);
             slot_sync();
             // phase 4
             issue_b(L, smem, 1, s + 2, wave);
             read_b<0>(rb, P ^ 1, fb0);
-            phase_sync<11>();
-            mma_quadrant<0>(acc[3], fa, fb1, sa, sb1);
+            phase_sync<10 + kS>();
+            mma_quadrant<FP4>(acc[3], fa, fb1, sa, sb1);
             slot_sync();
             r0 = r1;
         }
@@ -426,7 +485,7 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
 // pass, so each workgroup stays on the XCD map_tile assigns its tiles to).
 // The epilogue stores of one tile drain while the next tile's first copies
 // are in flight, instead of behind a workgroup exit and a new launch.
-template <bool BPS>
+template <bool BPS, bool FP4>
 __global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
 void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws, int tiles_x, int tiles_y)
 {
@@ -453,7 +512,7 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws, int tiles_x, int
     for (int lin = blockIdx.x; lin < ntiles; lin += gridDim.x) {
         int tile_m, tile_n;
         map_tile_lin(lin, tiles_x, tiles_y, kPpGroupM, tile_m, tile_n);
-        pp_tile<BPS>(a, ws, smem, tile_m, tile_n);
+        pp_tile<BPS, FP4>(a, ws, smem, tile_m, tile_n);
     }
     wait_vmcnt<0>(); // copies of steps past the last slice land before exit
 }
@@ -478,15 +537,29 @@ int pp_grid(int tiles)
 void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                       hipStream_t stream)
 {
-    hipLaunchKernelGGL(mx_pp_kernel<true>, dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT), 0, stream,
-                       args, ws, gdx, gdy);
+    hipLaunchKernelGGL((mx_pp_kernel<true, false>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
+                       0, stream, args, ws, gdx, gdy);
 }
 
 void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
                         hipStream_t stream)
 {
-    hipLaunchKernelGGL(mx_pp_kernel<false>, dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT), 0, stream,
-                       args, ws, gdx, gdy);
+    hipLaunchKernelGGL((mx_pp_kernel<false, false>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
+                       0, stream, args, ws, gdx, gdy);
+}
+
+void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                       hipStream_t stream)
+{
+    hipLaunchKernelGGL((mx_pp_kernel<true, true>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
+                       0, stream, args, ws, gdx, gdy);
+}
+
+void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                         hipStream_t stream)
+{
+    hipLaunchKernelGGL((mx_pp_kernel<false, true>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
+                       0, stream, args, ws, gdx, gdy);
 }
 
 } // namespace ga

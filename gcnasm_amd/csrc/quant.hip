@@ -83,6 +83,37 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ 
         s[(size_t)r * ld_s + b] = (uint8_t)(e + 127);
 }
 
+// ---- MXFP4: same blocking, e2m1 codes packed two per byte (low nibble = even
+// element), 16 bytes per 1x32 block ------------------------------------------
+template <int IN>
+__global__ __launch_bounds__(256) void quant_mx4_kernel(const void* __restrict__ x, int rows,
+                                                        int K, int ld_x, uint8_t* __restrict__ q,
+                                                        int ld_q, uint8_t* __restrict__ s,
+                                                        int ld_s, int rule)
+{
+    const int nb = K / 32;
+    const long long blk = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int sub = threadIdx.x & 7;
+    const bool valid = blk < (long long)rows * nb;
+    const int r = valid ? (int)(blk / nb) : 0;
+    const int b = valid ? (int)(blk - (long long)r * nb) : 0;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid)
+        load4<IN>(x, (size_t)r * ld_x + b * 32 + sub * 4, v);
+    const float amax = group_max<8>(amax4(v));
+    if (!valid)
+        return;
+    const int e = mx4_scale_exp(amax, rule);
+    uint32_t c[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        c[j] = e2m1_encode(ldexpf(v[j], -e));
+    *(uint16_t*)(q + (size_t)r * ld_q + b * 16 + sub * 2) =
+        (uint16_t)(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
+    if (sub == 0)
+        s[(size_t)r * ld_s + b] = (uint8_t)(e + 127);
+}
+
 // ---- DeepSeek 1x128: 32 lanes per block ------------------------------------
 __device__ __forceinline__ float ds_scale(float amax) { return amax > 0.0f ? amax / 448.0f : 1.0f; }
 
@@ -292,6 +323,24 @@ ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x,
         return fail(GA_ERR_SHAPE, "quant_mxfp8: K %% 32, ld_x %% 4 and ld_q %% 4 must be 0");
     long long blocks = (long long)rows * (K / 32);
     GA_DISPATCH_IN(in_dtype, quant_mx_kernel, dim3(grid1d(blocks, 32)), dim3(256), 0,
+                   (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q, (uint8_t*)scales,
+                   ld_s, scale_rule);
+    GA_HIP_CHECK(hipGetLastError());
+    return GA_OK;
+}
+
+ga_status ga_quant_mxfp4(const void* x, int in_dtype, int rows, int K, int ld_x, void* q,
+                         int ld_q, void* scales, int ld_s, int scale_rule, void* stream)
+{
+    if (check_in(in_dtype) != GA_OK)
+        return GA_ERR_ARG;
+    if (!x || !q || !scales || rows <= 0 || K <= 0 || ld_x < K || ld_q < K / 2 ||
+        ld_s < K / 32 || scale_rule < 0 || scale_rule > 2)
+        return fail(GA_ERR_ARG, "quant_mxfp4: bad argument");
+    if (K % 32 || ld_x % 4 || ld_q % 2)
+        return fail(GA_ERR_SHAPE, "quant_mxfp4: K %% 32, ld_x %% 4 and ld_q %% 2 must be 0");
+    long long blocks = (long long)rows * (K / 32);
+    GA_DISPATCH_IN(in_dtype, quant_mx4_kernel, dim3(grid1d(blocks, 32)), dim3(256), 0,
                    (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q, (uint8_t*)scales,
                    ld_s, scale_rule);
     GA_HIP_CHECK(hipGetLastError());

@@ -66,6 +66,26 @@ def manifest_csv():
     return buf.value.decode()
 
 
+def manifest_fp4():
+    """The compiled MXFP4 manifest (e2m1 operands), in manifest order."""
+    l = lib()
+    out = []
+    for i in range(l.ga_manifest_fp4_count()):
+        c = _lib.TileConfig()
+        check(l.ga_manifest_fp4_get(i, ctypes.byref(c)))
+        out.append(Config.from_c(c))
+    return out
+
+
+def manifest_fp4_csv():
+    l = lib()
+    need = ctypes.c_size_t(0)
+    check(l.ga_manifest_fp4_csv(None, 0, ctypes.byref(need)))
+    buf = ctypes.create_string_buffer(need.value)
+    check(l.ga_manifest_fp4_csv(buf, need.value, ctypes.byref(need)))
+    return buf.value.decode()
+
+
 def load_configs(csv_path):
     l = lib()
     n = ctypes.c_int(0)

@@ -30,6 +30,18 @@ def quant_mxfp8(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
     return q, s
 
 
+def quant_mxfp4(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
+    """x [rows, K] -> (q uint8 [rows, K/2] packed e2m1, low nibble = even element;
+    scales uint8 [rows, K/32] E8M0, unshuffled). Rule numbers as for MXFP8 with
+    the e2m1 maximum 6 in place of 448."""
+    rows, K = x.shape
+    q = torch.empty((rows, K // 2), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+    check(lib().ga_quant_mxfp4(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0), q.data_ptr(),
+                               K // 2, s.data_ptr(), K // 32, scale_rule, _stream_handle(stream)))
+    return q, s
+
+
 def quant_fp8_1x128(x, stream=None):
     """x [rows, K] -> (q [rows, K], sfa fp32 [K/128, rows])."""
     rows, K = x.shape
@@ -109,6 +121,47 @@ def prepare_mx_b(w, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, bpreshuffle=True, str
     codes = shuffle_weight_16x16(q, stream) if bpreshuffle else q
     ss = shuffle_scale(s, sh.scale_b_rows(), sh.scale_cols(), stream)
     return MxOperand(codes, ss, N, K)
+
+
+def prepare_mx4_a(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
+    """Activation [M, K] -> MXFP4 MxOperand: packed e2m1 [round_up(M, 256), K/2]."""
+    M, K = x.shape
+    sh = Shape(M, 1, K, elem_bits=4)
+    q, s = quant_mxfp4(x, scale_rule, stream)
+    codes = torch.zeros((sh.a_rows_pad(), K // 2), dtype=torch.uint8, device=x.device)
+    codes[:M].copy_(q)
+    ss = shuffle_scale(s, sh.scale_a_rows(), sh.scale_cols(), stream)
+    return MxOperand(codes, ss, M, K)
+
+
+def prepare_mx4_b(w, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, bpreshuffle=True, stream=None):
+    """Weight [N, K] -> MXFP4 MxOperand (packed bytes 16x16 preshuffled over Kp = K/2)."""
+    N, K = w.shape
+    sh = Shape(1, N, K, elem_bits=4)
+    q, s = quant_mxfp4(w, scale_rule, stream)
+    codes = shuffle_weight_16x16(q, stream) if bpreshuffle else q
+    ss = shuffle_scale(s, sh.scale_b_rows(), sh.scale_cols(), stream)
+    return MxOperand(codes, ss, N, K)
+
+
+def mxfp4_gemm(a, b, bpreshuffle=True, log2_k_split=0, out=None, num_cu=0, workspace=None,
+               stream=None):
+    """D [M, N] bf16 = A * B^T for MXFP4 operands (prepare_mx4_a/b) through the
+    MXFP4 manifest. Returns (D, registry index, launch desc)."""
+    M, N, K = a.rows, b.rows, a.K
+    sh = Shape(M, N, K, elem_bits=4)
+    if out is None:
+        out = torch.empty((sh.d_rows_pad(), N), dtype=torch.bfloat16, device=a.codes.device)
+    chosen = ctypes.c_int(-1)
+    ld = _lib.LaunchDesc()
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    check(lib().ga_mxfp4_gemm(out.data_ptr(), a.codes.data_ptr(), b.codes.data_ptr(),
+                              a.scales.data_ptr(), b.scales.data_ptr(), M, N, K, out.stride(0),
+                              int(bpreshuffle), log2_k_split, num_cu, ws_ptr, ws_bytes,
+                              ctypes.byref(chosen), ctypes.byref(ld), _stream_handle(stream)))
+    return out, chosen.value, ld
 
 
 def mxfp8_gemm(a, b, bpreshuffle=True, log2_k_split=0, out=None, num_cu=0, workspace=None,

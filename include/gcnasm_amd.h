@@ -142,6 +142,15 @@ ga_status ga_manifest_get(int idx, ga_tile_config* out);
  * *needed receives the byte count including the terminating NUL. */
 ga_status ga_manifest_csv(char* buf, size_t cap, size_t* needed);
 
+/* The MXFP4 manifest: the role of the reference's f4gemm_bf16_per1x32Fp4.csv
+ * (asm_f4gemm/README.md:30-40), same columns. Its kernels take OCP e2m1
+ * operands packed two per byte (low nibble = even element; A/B strides and
+ * K count elements, asm_f4gemm/README.md:86). Select from it by passing
+ * its rows to ga_select_kernel, then ga_kernel_find(knl_name). */
+int ga_manifest_fp4_count(void);
+ga_status ga_manifest_fp4_get(int idx, ga_tile_config* out);
+ga_status ga_manifest_fp4_csv(char* buf, size_t cap, size_t* needed);
+
 /* f4gemm::load_configs (f4gemm.hpp:141-200): parse a manifest CSV file. The
  * column order comes from the header row; rows whose column count differs
  * from the header are skipped; rows without knl_name or co_name are dropped.
@@ -216,6 +225,8 @@ ga_status ga_shuffle_scale_device(const void* src, void* dst, int rows, int cols
 #define GA_MX_SCALE_FLOOR_448 0 /* e = floor(log2(amax / 448)), literal config rule */
 #define GA_MX_SCALE_CEIL_448  1 /* e = ceil(log2(amax / 448)), never saturates     */
 #define GA_MX_SCALE_OCP       2 /* e = floor(log2(amax)) - 8, OCP MX v1.0          */
+/* For MXFP4 (ga_quant_mxfp4) the same rule numbers use the e2m1 maximum 6:
+ * 0: floor(log2(amax / 6)), 1: ceil(log2(amax / 6)), 2: floor(log2(amax)) - 2. */
 
 /* Input element types of the quantisers. */
 #define GA_IN_F32  0
@@ -225,6 +236,13 @@ ga_status ga_shuffle_scale_device(const void* src, void* dst, int rows, int cols
  * E4M3 (row stride ld_q bytes) and scales [rows, K/32] E8M0 (row stride
  * ld_s bytes), unshuffled. K % 32 == 0. */
 ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x,
+                         void* q, int ld_q, void* scales, int ld_s, int scale_rule,
+                         void* stream);
+/* MXFP4 quantiser: x [rows, K] -> q [rows, K/2] bytes of OCP e2m1 codes
+ * (element 2i in the low nibble of byte i, asm_f4gemm/README.md:99; round to
+ * nearest even, saturate to +-6, NaN -> signed zero; row stride ld_q bytes)
+ * and scales [rows, K/32] E8M0 (rules above), unshuffled. K % 32 == 0. */
+ga_status ga_quant_mxfp4(const void* x, int in_dtype, int rows, int K, int ld_x,
                          void* q, int ld_q, void* scales, int ld_s, int scale_rule,
                          void* stream);
 /* DeepSeek activation quantiser: per 1x128 block along K, s = amax/448 (fp32),
@@ -256,7 +274,9 @@ size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N
 /* Kernel::launch (f4gemm.hpp:297-309): D[M,N] bf16 = alpha*A*B^T (+beta*C).
  * A [M, K] E4M3 row-major (stride_A0 elements), B [N, K] E4M3, preshuffled
  * when the kernel's bpreshuffle is 1, ScaleA/ScaleB E8M0 padded+shuffled
- * (stride_ScaleX0 = padded column count). With gdz > 1 the K-slices are
+ * (stride_ScaleX0 = padded column count). MXFP4 kernels: A [M, K/2] and
+ * B [N, K/2] bytes of packed e2m1 (B preshuffled over Kp = K/2 bytes),
+ * strides still in elements, K % 256 == 0. With gdz > 1 the K-slices are
  * summed in fp32 in `workspace` (ga_kernel_workspace_bytes) and a reduce
  * kernel writes bf16 D; D need not be pre-zeroed. workspace == NULL with
  * gdz > 1 uses a library-owned per-device buffer (grown on demand; not safe
@@ -269,6 +289,15 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
  * log2_k_split as in ga_select_kernel. Writes the chosen kernel index and
  * launch into *chosen / *ld_out when non-NULL. */
 ga_status ga_mxfp8_gemm(void* d_D, const void* d_A, const void* d_B,
+                        const void* d_ScaleA, const void* d_ScaleB, int M, int N, int K,
+                        int stride_D0, int bpreshuffle, int log2_k_split, int num_cu,
+                        void* workspace, size_t workspace_bytes, int* chosen,
+                        ga_launch_desc* ld_out, void* stream);
+
+/* The same over the MXFP4 manifest (asm_f4gemm/main.cpp's flow for its
+ * f4gemm_bf16_per1x32Fp4 kernels): A/B packed e2m1, *chosen is the registry
+ * index (ga_kernel_find numbering). */
+ga_status ga_mxfp4_gemm(void* d_D, const void* d_A, const void* d_B,
                         const void* d_ScaleA, const void* d_ScaleB, int M, int N, int K,
                         int stride_D0, int bpreshuffle, int log2_k_split, int num_cu,
                         void* workspace, size_t workspace_bytes, int* chosen,

@@ -34,6 +34,11 @@ _SIGS = {
     "or_f32_to_bf16": (_u16, [_f]),
     "or_bf16_to_f32": (_f, [_u16]),
     "or_fp4_decode": (_f, [_u8]),
+    "or_e2m1_encode": (_u8, [_f]),
+    "or_mx4_scale_exp": (_i, [_f, _i]),
+    "or_quant_mxfp4": (None, [_vp, _i, _i, _vp, _vp, _i]),
+    "or_gemm_mx_exact": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "or_gemm_mx_fp32acc": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
     "or_floor_log2": (_i, [_f]),
     "or_mx_scale_exp": (_i, [_f, _i]),
     "or_quant_mxfp8": (None, [_vp, _i, _i, _vp, _vp, _i]),
@@ -145,6 +150,63 @@ def quant_mxfp8(x, rule=0):
     s = np.empty((rows, K // 32), dtype=np.uint8)
     load().or_quant_mxfp8(p(x), rows, K, p(q), p(s), rule)
     return q, s
+
+
+def quant_mxfp4(x, rule=0):
+    """q [rows, K/2] packed e2m1 (low nibble = even element), s [rows, K/32]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, K = x.shape
+    q = np.empty((rows, K // 2), dtype=np.uint8)
+    s = np.empty((rows, K // 32), dtype=np.uint8)
+    load().or_quant_mxfp4(p(x), rows, K, p(q), p(s), rule)
+    return q, s
+
+
+def fp4_decode_table():
+    O = load()
+    return np.array([O.or_fp4_decode(c) for c in range(16)], dtype=np.float32)
+
+
+def unpack_fp4(q):
+    """[rows, K/2] packed bytes -> [rows, K] nibble codes."""
+    q = np.asarray(q, dtype=np.uint8)
+    out = np.empty((q.shape[0], q.shape[1] * 2), dtype=np.uint8)
+    out[:, 0::2] = q & 15
+    out[:, 1::2] = q >> 4
+    return out
+
+
+def mx4_dequant(q, s):
+    """f64 values of an MXFP4 operand (q [rows, K/2] packed, s [rows, K/32])."""
+    t = fp4_decode_table().astype(np.float64)
+    sc = e8m0_decode_table().astype(np.float64)
+    return t[unpack_fp4(q)] * np.repeat(sc[s], 32, axis=1)
+
+
+def mx4_absdot(qa, sa, qb, sb):
+    return np.abs(mx4_dequant(qa, sa)) @ np.abs(mx4_dequant(qb, sb)).T
+
+
+def gemm_mx_exact(qa, sa, qb, sb, elem_bits):
+    M = qa.shape[0]
+    K = qa.shape[1] * (2 if elem_bits == 4 else 1)
+    N = qb.shape[0]
+    D = np.empty((M, N), dtype=np.float64)
+    load().or_gemm_mx_exact(p(np.ascontiguousarray(qa)), p(np.ascontiguousarray(qb)),
+                            p(np.ascontiguousarray(sa)), p(np.ascontiguousarray(sb)), M, N, K,
+                            elem_bits, p(D))
+    return D
+
+
+def gemm_mx_fp32acc(qa, sa, qb, sb, elem_bits, log2_k_split=0, alpha=1.0):
+    M = qa.shape[0]
+    K = qa.shape[1] * (2 if elem_bits == 4 else 1)
+    N = qb.shape[0]
+    D = np.empty((M, N), dtype=np.float32)
+    load().or_gemm_mx_fp32acc(p(np.ascontiguousarray(qa)), p(np.ascontiguousarray(qb)),
+                              p(np.ascontiguousarray(sa)), p(np.ascontiguousarray(sb)), M, N, K,
+                              elem_bits, log2_k_split, alpha, p(D))
+    return D
 
 
 def quant_fp8_1x128(x):

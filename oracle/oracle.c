@@ -120,6 +120,37 @@ float or_fp4_decode(uint8_t nib)
     return lut[nib & 15];
 }
 
+/* OCP E2M1 encode (the kFp4Lut value set above): nearest value, ties to the
+ * even code, |x| > 6 saturates to 6; NaN -> zero with the sign bit of x (e2m1
+ * has no NaN). Written as the midpoints between consecutive values: 0.25
+ * (tie -> 0), 0.75 (-> 1.0), 1.25 (-> 1.0), 1.75 (-> 2.0), 2.5 (-> 2.0),
+ * 3.5 (-> 4.0), 5 (-> 4.0). */
+uint8_t or_e2m1_encode(float x)
+{
+    uint32_t u = f2u(x);
+    float a = u2f(u & 0x7FFFFFFFu);
+    uint8_t c;
+    if (a != a)
+        c = 0;
+    else if (a <= 0.25f)
+        c = 0;
+    else if (a < 0.75f)
+        c = 1;
+    else if (a <= 1.25f)
+        c = 2;
+    else if (a < 1.75f)
+        c = 3;
+    else if (a <= 2.5f)
+        c = 4;
+    else if (a < 3.5f)
+        c = 5;
+    else if (a <= 5.0f)
+        c = 6;
+    else
+        c = 7;
+    return (uint8_t)(((u >> 28) & 8u) | c);
+}
+
 int or_floor_log2(float a)
 {
     uint32_t u = f2u(a) & 0x7FFFFFFFu;
@@ -168,6 +199,30 @@ int or_mx_scale_exp(float amax, int rule)
     return e;
 }
 
+/* The same rules for E2M1 (max 6 = 1.5 * 2^2, fraction bits 0x400000):
+ * 0 floor(log2(amax/6)), 1 ceil(log2(amax/6)), 2 OCP floor(log2 amax) - 2. */
+int or_mx4_scale_exp(float amax, int rule)
+{
+    if (!(amax > 0.0f))
+        return -127;
+    if (isinf(amax))
+        return 127;
+    int E = or_floor_log2(amax);
+    uint32_t f = frac_bits(amax);
+    int e;
+    if (rule == 0)
+        e = (f >= 0x400000u) ? E - 2 : E - 3;
+    else if (rule == 1)
+        e = (f <= 0x400000u) ? E - 2 : E - 1;
+    else
+        e = E - 2;
+    if (e < -127)
+        e = -127;
+    if (e > 127)
+        e = 127;
+    return e;
+}
+
 /* ------------------------------------------------------------------------- */
 /* Quantisers                                                                 */
 /* ------------------------------------------------------------------------- */
@@ -187,6 +242,30 @@ void or_quant_mxfp8(const float* x, int rows, int K, uint8_t* q, uint8_t* scales
             scales[(size_t)r * nb + b] = (uint8_t)(e + 127);
             for (int i = 0; i < 32; i++)
                 q[(size_t)r * K + b * 32 + i] = or_e4m3_encode(ldexpf(xb[i], -e));
+        }
+}
+
+/* MXFP4: same blocking; codes packed two per byte, element 2i in the low
+ * nibble of byte i (asm_f4gemm/README.md:97-99). q is [rows, K/2]. */
+void or_quant_mxfp4(const float* x, int rows, int K, uint8_t* q, uint8_t* scales, int rule)
+{
+    int nb = K / 32;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const float* xb = x + (size_t)r * K + b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) {
+                float a = fabsf(xb[i]);
+                if (a > amax)
+                    amax = a;
+            }
+            int e = or_mx4_scale_exp(amax, rule);
+            scales[(size_t)r * nb + b] = (uint8_t)(e + 127);
+            for (int i = 0; i < 32; i += 2) {
+                uint8_t lo = or_e2m1_encode(ldexpf(xb[i], -e));
+                uint8_t hi = or_e2m1_encode(ldexpf(xb[i + 1], -e));
+                q[(size_t)r * (K / 2) + (b * 32 + i) / 2] = (uint8_t)(lo | (hi << 4));
+            }
         }
 }
 
@@ -372,17 +451,30 @@ void or_reference_gemm(const float* A, const float* B, int M, int N, int K, floa
         }
 }
 
-/* Dequantised MX operand in f64: value * 2^(scale-127), exact. */
-static double* mx_dequant(const uint8_t* q, const uint8_t* s, int rows, int K)
+/* Dequantised MX operand in f64: value * 2^(scale-127), exact. elem_bits 8:
+ * E4M3 bytes [rows, K]; 4: e2m1 packed [rows, K/2], low nibble first. */
+static double* mx_dequant_bits(const uint8_t* q, const uint8_t* s, int rows, int K,
+                               int elem_bits)
 {
     double* d = (double*)malloc((size_t)rows * K * sizeof(double));
     for (int r = 0; r < rows; r++)
         for (int k = 0; k < K; k++) {
             uint8_t sc = s[(size_t)r * (K / 32) + k / 32];
-            d[(size_t)r * K + k] = (double)or_e4m3_decode(q[(size_t)r * K + k]) *
-                                   (double)or_e8m0_to_f32(sc);
+            double v;
+            if (elem_bits == 4) {
+                uint8_t byte = q[(size_t)r * (K / 2) + k / 2];
+                v = (double)or_fp4_decode((uint8_t)((k & 1) ? byte >> 4 : byte & 15));
+            } else {
+                v = (double)or_e4m3_decode(q[(size_t)r * K + k]);
+            }
+            d[(size_t)r * K + k] = v * (double)or_e8m0_to_f32(sc);
         }
     return d;
+}
+
+static double* mx_dequant(const uint8_t* q, const uint8_t* s, int rows, int K)
+{
+    return mx_dequant_bits(q, s, rows, K, 8);
 }
 
 static double* fp8_dequant(const uint8_t* q, int rows, int K, int ld)
@@ -404,11 +496,11 @@ static long double dot_ld(const double* a, const double* b, int k0, int k1)
     return s;
 }
 
-void or_gemm_mxfp8_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
-                         const uint8_t* sB, int M, int N, int K, double* D)
+void or_gemm_mx_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                      const uint8_t* sB, int M, int N, int K, int elem_bits, double* D)
 {
-    double* da = mx_dequant(A, sA, M, K);
-    double* db = mx_dequant(B, sB, N, K);
+    double* da = mx_dequant_bits(A, sA, M, K, elem_bits);
+    double* db = mx_dequant_bits(B, sB, N, K, elem_bits);
 #pragma omp parallel for schedule(static)
     for (int m = 0; m < M; m++)
         for (int n = 0; n < N; n++)
@@ -418,12 +510,12 @@ void or_gemm_mxfp8_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
     free(db);
 }
 
-void or_gemm_mxfp8_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
-                           const uint8_t* sB, int M, int N, int K, int log2_k_split,
-                           float alpha, float* D)
+void or_gemm_mx_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                        const uint8_t* sB, int M, int N, int K, int elem_bits, int log2_k_split,
+                        float alpha, float* D)
 {
-    double* da = mx_dequant(A, sA, M, K);
-    double* db = mx_dequant(B, sB, N, K);
+    double* da = mx_dequant_bits(A, sA, M, K, elem_bits);
+    double* db = mx_dequant_bits(B, sB, N, K, elem_bits);
     int k_num = 1 << log2_k_split;
     int kpt = ((K / k_num + 255) / 256) * 256;
     int gdz = (K + kpt - 1) / kpt;
@@ -446,6 +538,19 @@ void or_gemm_mxfp8_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA
         }
     free(da);
     free(db);
+}
+
+void or_gemm_mxfp8_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                         const uint8_t* sB, int M, int N, int K, double* D)
+{
+    or_gemm_mx_exact(A, B, sA, sB, M, N, K, 8, D);
+}
+
+void or_gemm_mxfp8_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                           const uint8_t* sB, int M, int N, int K, int log2_k_split,
+                           float alpha, float* D)
+{
+    or_gemm_mx_fp32acc(A, B, sA, sB, M, N, K, 8, log2_k_split, alpha, D);
 }
 
 static inline float sfb_at(const float* sfb, int g, int n, int stride_sfb, int group_n)

@@ -27,14 +27,20 @@ float or_e8m0_to_f32(uint8_t e);      /* f4gemm_ref.hpp:29-41                   
 uint16_t or_f32_to_bf16(float x);     /* RNE, opus.hpp:944-950                         */
 float or_bf16_to_f32(uint16_t h);     /* f4gemm_ref.hpp:43-49                          */
 float or_fp4_decode(uint8_t nibble);  /* kFp4Lut, f4gemm_ref.hpp:24-26                 */
+uint8_t or_e2m1_encode(float x);      /* OCP E2M1 RNE, saturate +-6, NaN -> signed 0  */
 int or_floor_log2(float a);           /* exact, a > 0 finite (normal or subnormal)     */
 
 /* E8M0 exponent of an MX block from its amax (rule: 0 floor448, 1 ceil448,
  * 2 OCP). Returns the unbiased exponent e; code = e + 127 (clamped). */
 int or_mx_scale_exp(float amax, int rule);
+/* Same rules for E2M1 elements (max 6): floor/ceil(log2(amax/6)), OCP - 2. */
+int or_mx4_scale_exp(float amax, int rule);
 
 /* ---- quantisers --------------------------------------------------------- */
 void or_quant_mxfp8(const float* x, int rows, int K, uint8_t* q, uint8_t* scales, int rule);
+/* MXFP4: q [rows, K/2] packed e2m1 (element 2i in the low nibble of byte i,
+ * asm_f4gemm/README.md:97-99), scales [rows, K/32]. */
+void or_quant_mxfp4(const float* x, int rows, int K, uint8_t* q, uint8_t* scales, int rule);
 void or_quant_fp8_1x128(const float* x, int rows, int K, uint8_t* q, float* sfa /*[K/128, rows]*/);
 void or_quant_fp8_128x128(const float* x, int rows, int K, uint8_t* q,
                           float* sfb /*[ceil(rows/128), K/128]*/);
@@ -66,6 +72,13 @@ void or_reference_gemm(const float* A, const float* B, int M, int N, int K, floa
 void or_gemm_mxfp8_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
                          const uint8_t* sB, int M, int N, int K, double* D);
 
+/* The two MX GEMMs above/below for either element width: elem_bits 8 (E4M3
+ * bytes [rows, K]) or 4 (e2m1 packed [rows, K/2], low nibble first). */
+void or_gemm_mx_exact(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                      const uint8_t* sB, int M, int N, int K, int elem_bits, double* D);
+void or_gemm_mx_fp32acc(const uint8_t* A, const uint8_t* B, const uint8_t* sA,
+                        const uint8_t* sB, int M, int N, int K, int elem_bits, int log2_k_split,
+                        float alpha, float* D);
 /* MXFP8 with fp32 accumulation in the order of the GPU kernel: K is cut into
  * gdz slices of k_per_tg = round_up(K / 2^L, 256) (f4gemm.hpp:342-344); in a
  * slice, each 128-wide K step adds its exact product sum to an fp32

@@ -1,0 +1,168 @@
+"""GPU parity of the MXFP4 path (e2m1 operands behind the f4gemm ABI).
+
+The reference drives aiter's f4gemm_bf16_per1x32Fp4 code objects
+(asm_f4gemm/README.md:1-40); these tests follow its regression sweep
+(asm_f4gemm/run_tests.sh) on the MXFP4 manifest: heuristic shapes, every
+manifest kernel at M=300 N=2048 K=1024, split-K, edge tiles, and the device
+quantiser. Expected GEMM values come from oracle.gemm_mx_fp32acc(bits=4)
+(exact 128-K step sums accumulated in fp32 in the kernel's K order) rounded
+to bf16, under the tolerance of helpers.bf16_compare; quantised codes, scales
+and packing are compared bit for bit with the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gcnasm_amd import f4gemm, ops
+from gcnasm_amd._lib import GaError
+from helpers import bf16_compare
+
+pytestmark = pytest.mark.gpu
+
+
+def mx4_operands(M, N, K, seed=1, rule=0, spread=4):
+    xa = oracle.gen_mx_input(M, K, seed * 7919 + 1, 1.0, spread)
+    xb = oracle.gen_mx_input(N, K, seed * 7919 + 2, 1.0, spread)
+    qa, sa = oracle.quant_mxfp4(xa, rule)
+    qb, sb = oracle.quant_mxfp4(xb, rule)
+    return qa, sa, qb, sb
+
+
+def cfg4(name):
+    for c in f4gemm.manifest_fp4():
+        if c.knl_name == name:
+            return c
+    raise KeyError(name)
+
+
+def run_mx4(dev, qa, sa, qb, sb, cfg, log2_k_split=0):
+    M, Kp = qa.shape
+    K = 2 * Kp
+    N = qb.shape[0]
+    sh = f4gemm.Shape(M, N, K, elem_bits=4)
+    a_pad = np.zeros((sh.a_rows_pad(), Kp), dtype=np.uint8)
+    a_pad[:M] = qa
+    A = torch.from_numpy(a_pad).to(dev)
+    bh = f4gemm.shuffle_weight_16x16(qb, N, Kp) if cfg.bpreshuffle else qb.reshape(-1)
+    B = torch.from_numpy(np.ascontiguousarray(bh)).to(dev)
+    SA = torch.from_numpy(f4gemm.shuffle_scale(sa, M, K // 32, sh.scale_a_rows(),
+                                               sh.scale_cols())).to(dev)
+    SB = torch.from_numpy(f4gemm.shuffle_scale(sb, N, K // 32, sh.scale_b_rows(),
+                                               sh.scale_cols())).to(dev)
+    D = torch.full((sh.d_rows_pad(), N), float("nan"), dtype=torch.bfloat16, device=dev)
+    ld = f4gemm.make_launch(cfg, M, N, K, log2_k_split)
+    args = f4gemm.fill_args(D, None, A, B, SA, SB, M, N, K, N, sh.scale_cols(), sh.scale_cols(),
+                            1.0, 0.0, ld.log2_k_split)
+    k = f4gemm.Kernel().load(None, cfg)
+    print("launch %s M=%d N=%d K=%d grid=(%d,%d,%d)" % (cfg.knl_name, M, N, K, ld.gdx, ld.gdy,
+                                                         ld.gdz), flush=True)
+    k.launch(args, ld.gdx, ld.gdy, ld.gdz)
+    torch.cuda.synchronize()
+    return D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def check4(got, qa, sa, qb, sb, l2, label):
+    want = oracle.to_bf16_bits(oracle.gemm_mx_fp32acc(qa, sa, qb, sb, 4, l2))
+    ok, st = bf16_compare(got, want, oracle.mx4_absdot(qa, sa, qb, sb))
+    print("%s: exact=%.5f max_ulp=%d bounded=%d bad=%d/%d" % (
+        label, st["exact"], st["max_ulp"], st["bounded"], st["bad"], st["n"]), flush=True)
+    assert st["bad"] == 0, "%s: %d outputs outside tolerance" % (label, st["bad"])
+    return st
+
+
+def test_manifest_fp4_rows():
+    rows = f4gemm.manifest_fp4()
+    assert [c.knl_name for c in rows] == ["ga_mxfp4_bf16_BpreShuffle_256x256",
+                                          "ga_mxfp4_bf16_BpreShuffle_256x256_splitK",
+                                          "ga_mxfp4_bf16_noBpreShuffle_256x256"]
+    assert f4gemm.manifest_fp4_csv().splitlines()[0] == \
+        "tile_M,tile_N,splitK,bpreshuffle,knl_name,co_name"
+
+
+@pytest.mark.parametrize("name", ["ga_mxfp4_bf16_BpreShuffle_256x256",
+                                  "ga_mxfp4_bf16_BpreShuffle_256x256_splitK",
+                                  "ga_mxfp4_bf16_noBpreShuffle_256x256"])
+def test_every_fp4_kernel(dev, name):
+    M, N, K = 300, 2048, 1024
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=3)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4(name))
+    st = check4(got, qa, sa, qb, sb, 0, name)
+    assert st["exact"] > 0.95
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 512), (1, 512, 256), (17, 784, 1280),
+                                   (520, 784, 2304), (256, 4096, 256), (2048, 1024, 1024)])
+def test_fp4_edge_shapes(dev, shape):
+    """Partial M and N tiles, one or an odd number of 256-K steps, one row."""
+    M, N, K = shape
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + N + K)
+    for name in ("ga_mxfp4_bf16_BpreShuffle_256x256", "ga_mxfp4_bf16_noBpreShuffle_256x256"):
+        got = run_mx4(dev, qa, sa, qb, sb, cfg4(name))
+        check4(got, qa, sa, qb, sb, 0, "%s %s" % (shape, name))
+
+
+@pytest.mark.parametrize("l2", [1, 2, 3])
+def test_fp4_splitk(dev, l2):
+    M, N, K = 96, 1024, 4096
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=7 + l2)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_BpreShuffle_256x256_splitK"), l2)
+    check4(got, qa, sa, qb, sb, l2, "splitK L=%d" % l2)
+
+
+def test_fp4_k_not_multiple_of_256_is_rejected(dev):
+    M, N, K = 64, 256, 384
+    sh = f4gemm.Shape(M, N, K, elem_bits=4)
+    A = torch.zeros((sh.a_rows_pad(), K // 2), dtype=torch.uint8, device=dev)
+    B = torch.zeros((N, K // 2), dtype=torch.uint8, device=dev)
+    S = torch.full((sh.scale_b_rows() * sh.scale_cols(),), 127, dtype=torch.uint8, device=dev)
+    D = torch.empty((sh.d_rows_pad(), N), dtype=torch.bfloat16, device=dev)
+    cfg = cfg4("ga_mxfp4_bf16_BpreShuffle_256x256")
+    ld = f4gemm.make_launch(cfg, M, N, K, 0)
+    args = f4gemm.fill_args(D, None, A, B, S, S, M, N, K, N, sh.scale_cols(), sh.scale_cols(),
+                            1.0, 0.0, 0)
+    with pytest.raises(GaError):
+        f4gemm.Kernel().load(None, cfg).launch(args, ld.gdx, ld.gdy, ld.gdz)
+
+
+def edge_input(rows, K, seed):
+    x = oracle.gen_mx_input(rows, K, seed, 1.0, 6)
+    flat = x.reshape(-1)
+    mids = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+    flat[:64] = np.concatenate([mids, -mids, [0.0, -0.0, 6.0, -6.0, 7.5, 1e-40, -1e-40,
+                                              np.inf, -np.inf, np.nan]]
+                               + [np.zeros(64 - 24, np.float32)])[:64]
+    x[1, :32] = 0.0                                  # zero block
+    x[2, :32] = np.float32(1e-42)                    # subnormal block
+    x[3, 5] = 6.0 * 2.0 ** 9                         # exact block maximum
+    return x
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
+def test_quant_mxfp4_bit_exact(dev, rule, in_dtype):
+    rows, K = 96, 1024
+    x = edge_input(rows, K, 40 + rule)
+    xt = torch.from_numpy(x).to(dev).to(in_dtype)
+    xr = xt.float().cpu().numpy()                    # the values the kernel sees
+    q, s = ops.quant_mxfp4(xt, scale_rule=rule)
+    wq, ws = oracle.quant_mxfp4(xr, rule)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+
+
+def test_mxfp4_gemm_one_call(dev):
+    """ops.mxfp4_gemm (device quantiser, device shuffles, heuristic over the MXFP4
+    manifest) against the oracle on the codes the device produced."""
+    M, N, K = 384, 1536, 2048
+    xa = torch.from_numpy(oracle.gen_mx_input(M, K, 5, 1.0, 4)).to(dev)
+    xb = torch.from_numpy(oracle.gen_mx_input(N, K, 6, 1.0, 4)).to(dev)
+    a = ops.prepare_mx4_a(xa)
+    b = ops.prepare_mx4_b(xb)
+    out, idx, ld = ops.mxfp4_gemm(a, b)
+    torch.cuda.synchronize()
+    qa, sa = ops.quant_mxfp4(xa)
+    qb, sb = ops.quant_mxfp4(xb)
+    got = out[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+    check4(got, qa.cpu().numpy(), sa.cpu().numpy(), qb.cpu().numpy(), sb.cpu().numpy(),
+           ld.log2_k_split, "one-call")
