@@ -45,7 +45,7 @@ void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gd
 // into registers, K slices summed in the workgroup (no workspace). Results
 // equal the tile kernels' (one fp32 chain of 128-K steps per slice).
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz);
-void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, int num_cu,
+void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,
                       hipStream_t stream);
 
 // Compute units of the current device (queried once per device).

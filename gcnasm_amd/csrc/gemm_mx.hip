@@ -319,7 +319,7 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
 #define GA_MX4_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                \
     {{256, 256, SPLIT, BPS, "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
-     &FN, 0, 4}
+     &FN, 64, 4}
 
 static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
@@ -457,7 +457,7 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         ga_status st = device_cu_count(&num_cu);
         if (st != GA_OK)
             return st;
-        launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, num_cu, s);
+        launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, num_cu, s);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;
     }

@@ -14,7 +14,10 @@
 //    workgroup and are summed in LDS in slice order (slice 0 first), the
 //    order the split-K reduce uses, so no workspace is needed;
 //  * workgroup = T column tasks x KS slices (T * KS = 4 waves, or KS waves
-//    for KS = 8).
+//    for KS = 8);
+//  * MXFP4 (e2m1 packed two per byte): a step is 256 K = the same 128 bytes
+//    per row, so the loads are identical; two fp4 MFMAs per group and 16
+//    rows (K halves 0 and 1 of the step), one whole scale dword per step.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
 #include <algorithm>
@@ -31,10 +34,11 @@ struct DecCfg {
 // Uniform byte offsets as SGPR operands.
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-template <int TM, int NG_, bool BPS>
+template <int TM, int NG_, bool BPS, bool FP4>
 __global__ __attribute__((amdgpu_flat_work_group_size(64, 512)))
 void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
 {
+    constexpr int kEPB = FP4 ? 2 : 1; // elements per byte
     constexpr int D = DecCfg<TM, NG_>::D, NG = NG_, NB = NG; // one scale dword per group
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
     constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
@@ -58,7 +62,8 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
     const int kb = slice * kpt;
     const int ke = min(K, kb + kpt);
-    const int nsteps = live ? max(0, (ke - kb) / 128) : 0;
+    const int nsteps = live ? max(0, (ke - kb) / (128 * kEPB)) : 0;
+    const int kbb = kb / kEPB, Kb = K / kEPB; // bytes
 
     v4f acc[NG][TM];
 #pragma unroll
@@ -69,33 +74,34 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
 
     if (nsteps > 0) {
         const int r = lane & 15, g = lane >> 4;
-        const uint32_t lda = args.stride_A0;
+        const uint32_t lda = args.stride_A0 / kEPB; // bytes
         long long abytes = (long long)M * lda;
         const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
         // A: lane 16g + r reads row 16i + r, K chunks g and g + 4 of the step
-        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kb;
+        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
         // B: groups past N read as zero (range-checked buffer)
         __amdgpu_buffer_rsrc_t rbuf;
         uint32_t vb, b_step, b_hi, b_grp;
         if (BPS) {
-            // group cg: K*16 contiguous bytes, [K/16][16 rows][16 B]
-            const char* pb = (const char*)args.ptr_B + (size_t)cg0 * K * 16;
-            rbuf = make_rsrc(pb, (uint32_t)ng_here * (uint32_t)K * 16);
-            vb = (uint32_t)lane * 16 + (uint32_t)kb * 16;
+            // group cg: Kb*16 contiguous bytes, [Kb/16][16 rows][16 B]
+            const char* pb = (const char*)args.ptr_B + (size_t)cg0 * Kb * 16;
+            rbuf = make_rsrc(pb, (uint32_t)ng_here * (uint32_t)Kb * 16);
+            vb = (uint32_t)lane * 16 + (uint32_t)kbb * 16;
             b_step = 2048;
             b_hi = 1024;
-            b_grp = (uint32_t)K * 16;
+            b_grp = (uint32_t)Kb * 16;
         } else {
-            const uint32_t ldb = args.stride_B0;
+            const uint32_t ldb = args.stride_B0 / kEPB; // bytes
             const char* pb = (const char*)args.ptr_B + (size_t)cg0 * 16 * ldb;
             rbuf = make_rsrc(pb, (uint32_t)ng_here * 16 * ldb);
-            vb = (uint32_t)r * ldb + g * 16 + (uint32_t)kb;
+            vb = (uint32_t)r * ldb + g * 16 + (uint32_t)kbb;
             b_step = 128;
             b_hi = 64;
             b_grp = 16 * ldb;
         }
         // scales: shuffled dword of lane l covers (row l%16 + 16 h, K block
-        // l/16) for 256 K; byte 2*(step parity) + h
+        // l/16) for 256 K; byte 2*(128-K half) + h (MXFP8: the half is the
+        // step parity; MXFP4: both halves in one step)
         const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
         const auto rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)((M + 31) / 32 * 32) * sna);
         const auto rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)((N + 31) / 32 * 32) * snb);
@@ -127,7 +133,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
                 v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
                 fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
             }
-            const uint32_t q = (uint32_t)(s >> 1) * 256;
+            const uint32_t q = (uint32_t)(FP4 ? s : (s >> 1)) * 256;
 #pragma unroll
             for (int h = 0; h < SA; h++)
                 fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
@@ -137,14 +143,22 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
         };
         auto mma = [&](int s, auto J) {
             constexpr int j = decltype(J)::value;
-            const uint32_t sh = (uint32_t)(s & 1) * 16;
+            const uint32_t sh = FP4 ? 0u : (uint32_t)(s & 1) * 16;
 #pragma unroll
             for (int c = 0; c < NG; c++) {
                 const uint32_t sb = fsb[j][c] >> (sh + 8 * ((cg0 + c) & 1));
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
                     const uint32_t sa = fsa[j][i >> 1] >> (sh + 8 * (i & 1));
-                    acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb, (int)sa);
+                    if constexpr (FP4) {
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
+                                                        (int)sa);
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(hi16(fb[j][c]), hi16(fa[j][i]), acc[c][i],
+                                                        (int)(sb >> 16), (int)(sa >> 16));
+                    } else {
+                        acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
+                                                    (int)sa);
+                    }
                 }
             }
         };
@@ -231,7 +245,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
 
 // Workgroups: one per CU (more when a CU's share needs over 8 waves), each
 // with ceil(share / NG) column tasks x ks slices.
-template <int TM, int NG, bool BPS>
+template <int TM, int NG, bool BPS, bool FP4>
 void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
@@ -240,8 +254,20 @@ void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t str
     nwg = std::max(nwg, (groups + NG * max_tasks - 1) / (NG * max_tasks));
     const int share = (groups + nwg - 1) / nwg;
     const int tasks = (share + NG - 1) / NG;
-    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS>), dim3(nwg), dim3(64 * tasks * ks), 0, stream,
-                       args, nwg, ks);
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4>), dim3(nwg), dim3(64 * tasks * ks), 0,
+                       stream, args, nwg, ks);
+}
+
+template <bool BPS, bool FP4>
+void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream_t stream)
+{
+    const int tm = ((int)args.M + 15) / 16;
+    if (tm == 1)
+        launch_dec<1, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    else if (tm == 2)
+        launch_dec<2, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    else
+        launch_dec<4, 2, BPS, FP4>(args, gdz, num_cu, stream);
 }
 
 } // namespace
@@ -251,24 +277,19 @@ bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz)
     return args.M >= 1 && args.M <= 64 && gdz <= 8;
 }
 
-void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, int num_cu,
+void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,
                       hipStream_t stream)
 {
-    const int tm = ((int)args.M + 15) / 16;
-    if (bps) {
-        if (tm == 1)
-            launch_dec<1, 2, true>(args, gdz, num_cu, stream);
-        else if (tm == 2)
-            launch_dec<2, 2, true>(args, gdz, num_cu, stream);
+    if (fp4) {
+        if (bps)
+            launch_dec_rows<true, true>(args, gdz, num_cu, stream);
         else
-            launch_dec<4, 2, true>(args, gdz, num_cu, stream);
+            launch_dec_rows<false, true>(args, gdz, num_cu, stream);
     } else {
-        if (tm == 1)
-            launch_dec<1, 2, false>(args, gdz, num_cu, stream);
-        else if (tm == 2)
-            launch_dec<2, 2, false>(args, gdz, num_cu, stream);
+        if (bps)
+            launch_dec_rows<true, false>(args, gdz, num_cu, stream);
         else
-            launch_dec<4, 2, false>(args, gdz, num_cu, stream);
+            launch_dec_rows<false, false>(args, gdz, num_cu, stream);
     }
 }
 

@@ -110,6 +110,27 @@ def test_fp4_splitk(dev, l2):
     check4(got, qa, sa, qb, sb, l2, "splitK L=%d" % l2)
 
 
+@pytest.mark.parametrize("M", [1, 16, 17, 33, 64])
+@pytest.mark.parametrize("NKL", [(784, 1280, 0), (784, 1280, 1), (4096, 2048, 0),
+                                 (4096, 2048, 2), (1808, 3072, 3)])
+def test_fp4_decode_path(dev, M, NKL):
+    """M <= 64 runs the streaming decode kernel (K slices summed in the
+    workgroup in slice order); results follow the same fp32 step chain."""
+    N, K, l2 = NKL
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M * 31 + N + l2)
+    name = ("ga_mxfp4_bf16_BpreShuffle_256x256_splitK" if l2 else
+            "ga_mxfp4_bf16_BpreShuffle_256x256")
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4(name), l2)
+    check4(got, qa, sa, qb, sb, l2, "decode M=%d N=%d K=%d L=%d" % (M, N, K, l2))
+
+
+def test_fp4_decode_plain_b(dev):
+    M, N, K = 16, 1024, 2048
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=77)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_noBpreShuffle_256x256"))
+    check4(got, qa, sa, qb, sb, 0, "decode plain B")
+
+
 def test_fp4_k_not_multiple_of_256_is_rejected(dev):
     M, N, K = 64, 256, 384
     sh = f4gemm.Shape(M, N, K, elem_bits=4)
