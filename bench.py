@@ -13,6 +13,10 @@ Also measured (reported in "decode"): the decode GEMMs M=16, N=28672, K=8192
 and M=16, N=8192, K=28672 with weights from N(0, 0.02), rotating 3 weight sets
 (> 256 MB Infinity Cache), at the reference driver's default log2_k_split=0.
 
+"mxfp4" / "mxfp4_decode" run the same two workloads with OCP e2m1 operands
+(the reference's own f4gemm kernels are MXFP4; its published 8192^3 figure,
+asm_f4gemm/README.md:171, is reported next to ours).
+
 "blockscale" times the DeepSeek-style GEMM (1x128 activation / 128x128 weight
 fp32 scales, fp32 C, opus_gemm kargs) at 8192^3 next to the reference's own
 published number for it (opus_gemm/block_scale_gemm/README.md:114), and the
@@ -36,6 +40,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 FP8_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 / MXFP8 MFMA (published)
+FP4_PEAK_TFLOPS = 10100.0  # MI355X dense FP4 / MXFP4 MFMA (published)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E (published)
 
 
@@ -52,7 +57,7 @@ def parse():
     return ap.parse_args()
 
 
-def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0):
+def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0, elem_bits=8):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -62,19 +67,24 @@ def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0):
         u = torch.randint(-4, 5, (rows, K // 32, 1), device=dev, generator=g).float()
         return (x.view(rows, K // 32, 32) * torch.exp2(u)).view(rows, K)
 
-    a = ops.prepare_mx_a(mx_input(M))
-    bs = [ops.prepare_mx_b(mx_input(N) * b_std) for _ in range(nsets)]
+    prep_a, prep_b = ((ops.prepare_mx_a, ops.prepare_mx_b) if elem_bits == 8 else
+                      (ops.prepare_mx4_a, ops.prepare_mx4_b))
+    a = prep_a(mx_input(M))
+    bs = [prep_b(mx_input(N) * b_std) for _ in range(nsets)]
     torch.cuda.synchronize()
     return a, bs
 
 
-def time_gemm(torch, f4gemm, a, bs, M, N, K, steps, warmup, log2_k_split=0, name=None):
-    sh = f4gemm.Shape(M, N, K)
+def time_gemm(torch, f4gemm, a, bs, M, N, K, steps, warmup, log2_k_split=0, name=None,
+              elem_bits=8):
+    sh = f4gemm.Shape(M, N, K, elem_bits=elem_bits)
+    table = f4gemm.manifest() if elem_bits == 8 else f4gemm.manifest_fp4()
     if name is None:
-        idx, l2 = f4gemm.select_kernel(M, N, K, 256, log2_k_split, 1)
-        cfg = f4gemm.manifest()[idx]
+        idx, l2 = f4gemm.select_kernel(M, N, K, 256, log2_k_split, 1,
+                                       cfgs=None if elem_bits == 8 else table)
+        cfg = table[idx]
     else:
-        cfg = [c for c in f4gemm.manifest() if c.knl_name == name][0]
+        cfg = [c for c in table if c.knl_name == name][0]
         l2 = max(log2_k_split, 0)
     ld = f4gemm.make_launch(cfg, M, N, K, l2)
     kern = f4gemm.Kernel().load(None, cfg)
@@ -149,6 +159,36 @@ def mfma_ceiling(torch, codes):
 
 
 REF_BLOCKSCALE_8192_TFLOPS = 2710.24  # opus_gemm/block_scale_gemm/README.md:114 (MI355X)
+REF_MXFP4_8192_TFLOPS = 4245.0         # asm_f4gemm/README.md:171 (MI355X, aiter code objects)
+
+
+def mxfp4_legs(torch, ops, f4gemm, steps, warmup):
+    """MXFP4 (e2m1) GEMM at 8192^3 and the M=16 decode shape, same protocol as
+    the MXFP8 legs (decode: 3 rotated weight sets, log2_k_split 0)."""
+    n = 8192
+    a, bs = mx_problem(torch, ops, f4gemm, n, n, n, seed=3, elem_bits=4)
+    r = time_gemm(torch, f4gemm, a, bs, n, n, n, steps, warmup, elem_bits=4)
+    del a, bs
+    torch.cuda.empty_cache()
+    tf = 2.0 * n ** 3 / (r["avg_us"] * 1e-6) / 1e12
+    big = {"workload": "mxfp4_gemm_8192x8192x8192", "value": round(tf, 1), "unit": "TFLOP/s",
+           "kernel": r["cfg"].knl_name, "kernel_avg_us": round(r["avg_us"], 2),
+           "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+           "reference_published": REF_MXFP4_8192_TFLOPS,
+           "vs_reference": round(tf / REF_MXFP4_8192_TFLOPS, 4)}
+    dM, dN, dK = 16, 28672, 8192
+    da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=4, elem_bits=4)
+    dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(steps, 30), warmup, log2_k_split=0,
+                   elem_bits=4)
+    del da, dbs
+    torch.cuda.empty_cache()
+    dbytes = dM * dK / 2 + dN * dK / 2 + (dM + dN) * dK / 32 + 2 * dM * dN
+    dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
+    dec = {"workload": "mxfp4_gemm_decode_%dx%dx%d" % (dM, dN, dK), "value": round(dgbs, 1),
+           "unit": "GB/s", "kernel": dr["cfg"].knl_name, "kernel_avg_us": round(dr["avg_us"], 2),
+           "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(dbytes),
+           "weight_sets": 3}
+    return big, dec
 
 
 def time_call(torch, fn, steps, warmup):
@@ -290,6 +330,7 @@ def main():
         torch.cuda.empty_cache()
 
     blockscale, per_tensor = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
+    mxfp4, mxfp4_decode = mxfp4_legs(torch, ops, f4gemm, 20, 5)
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
@@ -317,6 +358,8 @@ def main():
         "mfma_ceiling": ceiling,
         "blockscale": blockscale,
         "per_tensor": per_tensor,
+        "mxfp4": mxfp4,
+        "mxfp4_decode": mxfp4_decode,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
