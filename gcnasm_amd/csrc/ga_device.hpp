@@ -173,6 +173,41 @@ __device__ __forceinline__ uint32_t e4m3_encode(float x)
     return sign | (code > 0x7Eu ? 0x7Eu : code);
 }
 
+// Four E4M3 codes packed little-endian, same results as e4m3_encode: the
+// hardware converter (v_cvt_pk_fp8_f32: OCP E4M3, round to nearest even) on
+// inputs clamped to +-448 (saturation), NaN inputs replaced by 0x7F after.
+__device__ __forceinline__ uint32_t e4m3_encode4(float a, float b, float c, float d)
+{
+    const float x[4] = {a, b, c, d};
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        y[j] = __builtin_fminf(__builtin_fmaxf(x[j], -448.0f), 448.0f);
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        if (x[j] != x[j])
+            r = (r & ~(0xFFu << (8 * j))) | (0x7Fu << (8 * j));
+    return r;
+}
+
+// Four e2m1 codes as 16 bits (element j in bits 4j..4j+3), same results as
+// e2m1_encode: the hardware converter (v_cvt_scalef32_pk_fp4_f32, scale 1)
+// on inputs clamped to +-6, NaN inputs replaced by a zero of their sign.
+__device__ __forceinline__ uint32_t e2m1_encode4(float a, float b, float c, float d)
+{
+    const float x[4] = {a, b, c, d};
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        y[j] = x[j] != x[j] ? __builtin_copysignf(0.0f, x[j])
+                            : __builtin_fminf(__builtin_fmaxf(x[j], -6.0f), 6.0f);
+    uint32_t r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, y[0], y[1], 1.0f, 0);
+    r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, y[2], y[3], 1.0f, 1);
+    return r & 0xFFFFu;
+}
+
 // Exact floor(log2 a) and 23 fraction bits for a finite a > 0.
 __device__ __forceinline__ void log2_parts(float a, int& E, uint32_t& frac)
 {

@@ -9,24 +9,44 @@
 //   * per-tensor:     one fp32 s = amax/448
 // Encoding is the exact integer RNE/saturating E4M3 encode of ga_device.hpp;
 // x/s uses IEEE fp32 division (correctly rounded; built without fast-math).
-// All kernels are HBM streaming kernels: 16-byte (fp32) or 8-byte (bf16)
-// loads per lane, cross-lane amax with shuffles, coalesced code stores.
+// All kernels are HBM streaming kernels: 16-byte loads per lane (8-byte for
+// bf16 rows whose stride does not allow 16), several independent loads in
+// flight per lane, cross-lane amax over DPP row exchanges, coalesced stores.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
 
 namespace ga {
 
-template <int IN>
-__device__ __forceinline__ void load4(const void* x, size_t idx, float (&v)[4])
+__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
 {
-    if (IN == GA_IN_F32) {
-        v4f t = *(const v4f*)((const float*)x + idx);
-        v[0] = t[0];
-        v[1] = t[1];
-        v[2] = t[2];
-        v[3] = t[3];
+    return a | (b << 8) | (c << 16) | (d << 24);
+}
+
+// Up to 8 elements per lane from one 16-byte (f32: 4) or 8/16-byte (bf16: 4/8)
+// load; lanes that are out of range read zeros.
+template <int IN, int EPL>
+__device__ __forceinline__ void load_elems(const void* x, size_t idx, bool ok, float (&v)[EPL])
+{
+#pragma unroll
+    for (int j = 0; j < EPL; j++)
+        v[j] = 0.0f;
+    if (!ok)
+        return;
+    if constexpr (IN == GA_IN_F32) {
+        static_assert(EPL == 4, "f32: 4 elements per 16-byte load");
+        const v4f t = *(const v4f*)((const float*)x + idx);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v[j] = t[j];
+    } else if constexpr (EPL == 8) {
+        const v4i t = *(const v4i*)((const uint16_t*)x + idx);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = bf16_to_f32((uint16_t)((uint32_t)t[j] & 0xFFFF));
+            v[2 * j + 1] = bf16_to_f32((uint16_t)((uint32_t)t[j] >> 16));
+        }
     } else {
-        uint2 t = *(const uint2*)((const uint16_t*)x + idx);
+        const uint2 t = *(const uint2*)((const uint16_t*)x + idx);
         v[0] = bf16_to_f32((uint16_t)(t.x & 0xFFFF));
         v[1] = bf16_to_f32((uint16_t)(t.x >> 16));
         v[2] = bf16_to_f32((uint16_t)(t.y & 0xFFFF));
@@ -34,154 +54,212 @@ __device__ __forceinline__ void load4(const void* x, size_t idx, float (&v)[4])
     }
 }
 
-// NaN-ignoring max of |v| (fmaxf returns the non-NaN operand).
-__device__ __forceinline__ float amax4(const float (&v)[4])
+// Block maxima of |x| are taken on the bit patterns: for x >= 0 the IEEE bit
+// order is the value order, and every NaN (quiet or signalling) maps to 0, so
+// the maximum ignores NaNs exactly as the CPU reference's `a > amax` scan
+// does (a float max would turn a signalling NaN into a NaN result).
+__device__ __forceinline__ uint32_t abs_key(float x)
 {
-    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const uint32_t u = __float_as_uint(x) & 0x7FFFFFFFu;
+    return u > 0x7F800000u ? 0u : u;
 }
 
-template <int WIDTH>
-__device__ __forceinline__ float group_max(float a)
+template <int EPL>
+__device__ __forceinline__ uint32_t amax_n(const float (&v)[EPL])
 {
+    uint32_t a = abs_key(v[0]);
 #pragma unroll
-    for (int o = 1; o < WIDTH; o <<= 1)
-        a = fmaxf(a, __shfl_xor(a, o, 64));
+    for (int j = 1; j < EPL; j++)
+        a = max(a, abs_key(v[j]));
     return a;
 }
 
-__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+// Maximum over aligned groups of W lanes (W = 4, 8, 16, 32). Inside a 16-lane
+// row the exchange uses DPP (quad_perm xor 1 and xor 2, then the half- and
+// full-row mirrors, which pair each 4- / 8-lane group with its neighbour once
+// every lane of a group holds the group's max); across rows one swizzle.
+template <int W>
+__device__ __forceinline__ uint32_t group_max_dpp(uint32_t a)
 {
-    return a | (b << 8) | (c << 16) | (d << 24);
+    auto dpp = [](uint32_t v, auto ctrl) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, decltype(ctrl)::value, 0xF, 0xF,
+                                                     false);
+    };
+    a = max(a, dpp(a, std::integral_constant<int, 0xB1>{})); // quad_perm(1,0,3,2)
+    a = max(a, dpp(a, std::integral_constant<int, 0x4E>{})); // quad_perm(2,3,0,1)
+    if constexpr (W >= 8)
+        a = max(a, dpp(a, std::integral_constant<int, 0x141>{})); // row_half_mirror
+    if constexpr (W >= 16)
+        a = max(a, dpp(a, std::integral_constant<int, 0x140>{})); // row_mirror
+    if constexpr (W >= 32)
+        a = max(a, (uint32_t)__shfl_xor((int)a, 16, 64));
+    return a;
 }
 
-// ---- MX 1x32: 8 lanes per block, 4 elements per lane -----------------------
-template <int IN>
+// ---- MX 1x32 (E4M3 or packed e2m1 codes) -------------------------------------
+// A 1x32 block is LPB = 32/EPL lanes of EPL elements (16-byte loads where the
+// layout allows); each lane handles U blocks, BPP = 256/LPB blocks apart, so U
+// independent loads are in flight per lane before the first reduction.
+template <int IN, int EPL, bool FP4, int U>
 __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ x, int rows,
                                                        int K, int ld_x, uint8_t* __restrict__ q,
                                                        int ld_q, uint8_t* __restrict__ s,
                                                        int ld_s, int rule)
 {
+    constexpr int LPB = 32 / EPL, BPP = 256 / LPB;
     const int nb = K / 32;
-    const long long blk = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
-    const bool valid = blk < (long long)rows * nb;
-    const int r = valid ? (int)(blk / nb) : 0;
-    const int b = valid ? (int)(blk - (long long)r * nb) : 0;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid)
-        load4<IN>(x, (size_t)r * ld_x + b * 32 + sub * 4, v);
-    const float amax = group_max<8>(amax4(v));
-    if (!valid)
-        return;
-    const int e = mx_scale_exp(amax, rule);
-    uint32_t c[4];
+    const long long total = (long long)rows * nb;
+    const int sub = threadIdx.x % LPB;
+    const long long base = (long long)blockIdx.x * (BPP * U) + threadIdx.x / LPB;
+    float v[U][EPL];
+    int rr[U], bb[U];
+    bool ok[U];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        c[j] = e4m3_encode(ldexpf(v[j], -e));
-    *(uint32_t*)(q + (size_t)r * ld_q + b * 32 + sub * 4) = pack4(c[0], c[1], c[2], c[3]);
-    if (sub == 0)
-        s[(size_t)r * ld_s + b] = (uint8_t)(e + 127);
+    for (int u = 0; u < U; u++) {
+        const long long blk = base + (long long)u * BPP;
+        ok[u] = blk < total;
+        rr[u] = ok[u] ? (int)(blk / nb) : 0;
+        bb[u] = ok[u] ? (int)(blk - (long long)rr[u] * nb) : 0;
+        load_elems<IN, EPL>(x, (size_t)rr[u] * ld_x + bb[u] * 32 + sub * EPL, ok[u], v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const float amax = __uint_as_float(group_max_dpp<LPB>(amax_n<EPL>(v[u])));
+        if (!ok[u])
+            continue;
+        const int e = FP4 ? mx4_scale_exp(amax, rule) : mx_scale_exp(amax, rule);
+        uint8_t* qrow = q + (size_t)rr[u] * ld_q;
+        if constexpr (FP4) {
+            float t[EPL];
+#pragma unroll
+            for (int j = 0; j < EPL; j++)
+                t[j] = ldexpf(v[u][j], -e);
+            uint32_t w = e2m1_encode4(t[0], t[1], t[2], t[3]);
+            if constexpr (EPL == 8)
+                w |= e2m1_encode4(t[4], t[5], t[6], t[7]) << 16;
+            if constexpr (EPL == 8)
+                *(uint32_t*)(qrow + bb[u] * 16 + sub * 4) = w;
+            else
+                *(uint16_t*)(qrow + bb[u] * 16 + sub * 2) = (uint16_t)w;
+        } else {
+            float t[EPL];
+#pragma unroll
+            for (int j = 0; j < EPL; j++)
+                t[j] = ldexpf(v[u][j], -e);
+            if constexpr (EPL == 8) {
+                uint2 w;
+                w.x = e4m3_encode4(t[0], t[1], t[2], t[3]);
+                w.y = e4m3_encode4(t[4], t[5], t[6], t[7]);
+                *(uint2*)(qrow + bb[u] * 32 + sub * 8) = w;
+            } else {
+                *(uint32_t*)(qrow + bb[u] * 32 + sub * 4) = e4m3_encode4(t[0], t[1], t[2], t[3]);
+            }
+        }
+        if (sub == 0)
+            s[(size_t)rr[u] * ld_s + bb[u]] = (uint8_t)(e + 127);
+    }
 }
 
-// ---- MXFP4: same blocking, e2m1 codes packed two per byte (low nibble = even
-// element), 16 bytes per 1x32 block ------------------------------------------
-template <int IN>
-__global__ __launch_bounds__(256) void quant_mx4_kernel(const void* __restrict__ x, int rows,
-                                                        int K, int ld_x, uint8_t* __restrict__ q,
-                                                        int ld_q, uint8_t* __restrict__ s,
-                                                        int ld_s, int rule)
-{
-    const int nb = K / 32;
-    const long long blk = (long long)blockIdx.x * 32 + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
-    const bool valid = blk < (long long)rows * nb;
-    const int r = valid ? (int)(blk / nb) : 0;
-    const int b = valid ? (int)(blk - (long long)r * nb) : 0;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid)
-        load4<IN>(x, (size_t)r * ld_x + b * 32 + sub * 4, v);
-    const float amax = group_max<8>(amax4(v));
-    if (!valid)
-        return;
-    const int e = mx4_scale_exp(amax, rule);
-    uint32_t c[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-        c[j] = e2m1_encode(ldexpf(v[j], -e));
-    *(uint16_t*)(q + (size_t)r * ld_q + b * 16 + sub * 2) =
-        (uint16_t)(c[0] | (c[1] << 4) | (c[2] << 8) | (c[3] << 12));
-    if (sub == 0)
-        s[(size_t)r * ld_s + b] = (uint8_t)(e + 127);
-}
-
-// ---- DeepSeek 1x128: 32 lanes per block ------------------------------------
+// ---- DeepSeek 1x128 -----------------------------------------------------------
 __device__ __forceinline__ float ds_scale(float amax) { return amax > 0.0f ? amax / 448.0f : 1.0f; }
 
-template <int IN>
+// A 1x128 group is LPB = 128/EPL lanes; U groups per lane as above.
+template <int IN, int EPL, int U>
 __global__ __launch_bounds__(256) void quant_1x128_kernel(const void* __restrict__ x, int rows,
                                                           int K, int ld_x, uint8_t* __restrict__ q,
                                                           int ld_q, float* __restrict__ sfa,
                                                           int ld_s)
 {
+    constexpr int LPB = 128 / EPL, BPP = 256 / LPB;
     const int ng = K / 128;
-    const long long blk = (long long)blockIdx.x * 8 + (threadIdx.x >> 5);
-    const int sub = threadIdx.x & 31;
-    const bool valid = blk < (long long)rows * ng;
-    const int r = valid ? (int)(blk / ng) : 0;
-    const int g = valid ? (int)(blk - (long long)r * ng) : 0;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid)
-        load4<IN>(x, (size_t)r * ld_x + g * 128 + sub * 4, v);
-    const float amax = group_max<32>(amax4(v));
-    if (!valid)
-        return;
-    const float sc = ds_scale(amax);
-    uint32_t c[4];
+    const long long total = (long long)rows * ng;
+    const int sub = threadIdx.x % LPB;
+    const long long base = (long long)blockIdx.x * (BPP * U) + threadIdx.x / LPB;
+    float v[U][EPL];
+    int rr[U], gg[U];
+    bool ok[U];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        c[j] = e4m3_encode(v[j] / sc);
-    *(uint32_t*)(q + (size_t)r * ld_q + g * 128 + sub * 4) = pack4(c[0], c[1], c[2], c[3]);
-    if (sub == 0)
-        sfa[(size_t)g * ld_s + r] = sc;
+    for (int u = 0; u < U; u++) {
+        const long long blk = base + (long long)u * BPP;
+        ok[u] = blk < total;
+        rr[u] = ok[u] ? (int)(blk / ng) : 0;
+        gg[u] = ok[u] ? (int)(blk - (long long)rr[u] * ng) : 0;
+        load_elems<IN, EPL>(x, (size_t)rr[u] * ld_x + gg[u] * 128 + sub * EPL, ok[u], v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const float amax = __uint_as_float(group_max_dpp<LPB>(amax_n<EPL>(v[u])));
+        if (!ok[u])
+            continue;
+        const float sc = ds_scale(amax);
+        float t[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; j++)
+            t[j] = v[u][j] / sc;
+        uint8_t* dst = q + (size_t)rr[u] * ld_q + gg[u] * 128 + sub * EPL;
+        if constexpr (EPL == 8) {
+            uint2 w;
+            w.x = e4m3_encode4(t[0], t[1], t[2], t[3]);
+            w.y = e4m3_encode4(t[4], t[5], t[6], t[7]);
+            *(uint2*)dst = w;
+        } else {
+            *(uint32_t*)dst = e4m3_encode4(t[0], t[1], t[2], t[3]);
+        }
+        if (sub == 0)
+            sfa[(size_t)gg[u] * ld_s + rr[u]] = sc;
+    }
 }
 
-// ---- DeepSeek 128x128: one workgroup per tile -------------------------------
-template <int IN>
+// ---- DeepSeek 128x128: one workgroup per tile ----------------------------------
+// The tile is read once into registers (64 values per lane: 16 / 8 loads in
+// flight), reduced in the workgroup, then quantised from registers.
+template <int IN, int EPL>
 __global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restrict__ x, int rows,
                                                             int K, int ld_x,
                                                             uint8_t* __restrict__ q, int ld_q,
                                                             float* __restrict__ sfb, int ld_s)
 {
-    __shared__ float wmax[4];
+    constexpr int LPR = 128 / EPL;     // lanes per tile row
+    constexpr int RPP = 256 / LPR;     // rows per pass
+    constexpr int NP = 128 / RPP;      // passes
+    __shared__ uint32_t wmax[4];
     const int g = blockIdx.x, rb = blockIdx.y;
     const int tid = threadIdx.x;
-    // 32 lanes span the 128 columns (4 each); 8 row slots, 16 rows per slot.
-    const int col = (tid & 31) * 4, r_lo = tid >> 5;
-    float amax = 0.0f;
-    for (int i = 0; i < 16; i++) {
-        const int r = rb * 128 + r_lo + i * 8;
-        if (r < rows) {
-            float v[4];
-            load4<IN>(x, (size_t)r * ld_x + g * 128 + col, v);
-            amax = fmaxf(amax, amax4(v));
-        }
+    const int col = (tid % LPR) * EPL, r_lo = tid / LPR;
+    float v[NP][EPL];
+    uint32_t amax = 0u;
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int r = rb * 128 + r_lo + i * RPP;
+        load_elems<IN, EPL>(x, (size_t)r * ld_x + g * 128 + col, r < rows, v[i]);
     }
-    amax = group_max<64>(amax);
+#pragma unroll
+    for (int i = 0; i < NP; i++)
+        amax = max(amax, amax_n<EPL>(v[i]));
+    amax = group_max_dpp<32>(amax);
+    amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32, 64));
     if ((tid & 63) == 0)
         wmax[tid >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const float sc = ds_scale(amax);
-    for (int i = 0; i < 16; i++) {
-        const int r = rb * 128 + r_lo + i * 8;
-        if (r < rows) {
-            float v[4];
-            load4<IN>(x, (size_t)r * ld_x + g * 128 + col, v);
-            uint32_t c[4];
+    amax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+    const float sc = ds_scale(__uint_as_float(amax));
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                c[j] = e4m3_encode(v[j] / sc);
-            *(uint32_t*)(q + (size_t)r * ld_q + g * 128 + col) = pack4(c[0], c[1], c[2], c[3]);
+    for (int i = 0; i < NP; i++) {
+        const int r = rb * 128 + r_lo + i * RPP;
+        if (r >= rows)
+            continue;
+        float t[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; j++)
+            t[j] = v[i][j] / sc;
+        uint8_t* dst = q + (size_t)r * ld_q + g * 128 + col;
+        if constexpr (EPL == 8) {
+            uint2 w;
+            w.x = e4m3_encode4(t[0], t[1], t[2], t[3]);
+            w.y = e4m3_encode4(t[4], t[5], t[6], t[7]);
+            *(uint2*)dst = w;
+        } else {
+            *(uint32_t*)dst = e4m3_encode4(t[0], t[1], t[2], t[3]);
         }
     }
     if (tid == 0)
@@ -189,27 +267,39 @@ __global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restri
 }
 
 // ---- per-tensor: zero, amax (atomicMax on the bits of |x|), quantise --------
+// Both passes stream x with U loads of 16 bytes (f32) or 8 bytes (bf16) in
+// flight per lane; the scalar tail (n % 4) is handled by block 0.
+constexpr int kTensorU = 4;
+
 __global__ void zero_u32_kernel(uint32_t* p) { *p = 0u; }
 
 template <int IN>
 __global__ __launch_bounds__(256) void amax_kernel(const void* __restrict__ x, size_t n,
                                                    uint32_t* __restrict__ amax_bits)
 {
-    float a = 0.0f;
+    uint32_t a = 0u;
     const size_t n4 = n / 4;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-        float v[4];
-        load4<IN>(x, i * 4, v);
-        a = fmaxf(a, amax4(v));
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i0 = (size_t)blockIdx.x * 256 + threadIdx.x; i0 < n4; i0 += stride * kTensorU) {
+        float v[kTensorU][4];
+#pragma unroll
+        for (int u = 0; u < kTensorU; u++) {
+            const size_t i = i0 + u * stride;
+            load_elems<IN, 4>(x, i * 4, i < n4, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kTensorU; u++)
+            a = max(a, amax_n<4>(v[u]));
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         size_t i = n4 * 4 + threadIdx.x;
         float v = IN == GA_IN_F32 ? ((const float*)x)[i] : bf16_to_f32(((const uint16_t*)x)[i]);
-        a = fmaxf(a, fabsf(v));
+        a = max(a, abs_key(v));
     }
-    a = group_max<64>(a);
-    if ((threadIdx.x & 63) == 0 && a > 0.0f)
-        atomicMax(amax_bits, __float_as_uint(a));
+    a = group_max_dpp<32>(a);
+    a = max(a, (uint32_t)__shfl_xor((int)a, 32, 64));
+    if ((threadIdx.x & 63) == 0 && a > 0u)
+        atomicMax(amax_bits, a);
 }
 
 template <int IN>
@@ -222,11 +312,21 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const void* __restric
     if (blockIdx.x == 0 && threadIdx.x == 0)
         *scale = sc;
     const size_t n4 = n / 4;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
-        float v[4];
-        load4<IN>(x, i * 4, v);
-        *(uint32_t*)(q + i * 4) = pack4(e4m3_encode(v[0] / sc), e4m3_encode(v[1] / sc),
-                                        e4m3_encode(v[2] / sc), e4m3_encode(v[3] / sc));
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i0 = (size_t)blockIdx.x * 256 + threadIdx.x; i0 < n4; i0 += stride * kTensorU) {
+        float v[kTensorU][4];
+#pragma unroll
+        for (int u = 0; u < kTensorU; u++) {
+            const size_t i = i0 + u * stride;
+            load_elems<IN, 4>(x, i * 4, i < n4, v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kTensorU; u++) {
+            const size_t i = i0 + u * stride;
+            if (i < n4)
+                *(uint32_t*)(q + i * 4) = e4m3_encode4(v[u][0] / sc, v[u][1] / sc, v[u][2] / sc,
+                                                       v[u][3] / sc);
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         size_t i = n4 * 4 + threadIdx.x;
@@ -302,6 +402,36 @@ using namespace ga;
             hipLaunchKernelGGL(KERNEL<GA_IN_BF16>, __VA_ARGS__);                   \
     } while (0)
 
+constexpr int kQU = 4; // 1x32 / 1x128 blocks per lane
+
+// bf16 inputs use 16-byte loads (8 elements per lane) when the row stride and
+// base allow it and the codes' stores stay aligned (store_align: bytes per
+// lane store); otherwise 8-byte loads.
+static bool bf16_wide(int in_dtype, const void* x, int ld_x, const void* q, int ld_q,
+                      int store_align)
+{
+    return in_dtype == GA_IN_BF16 && ld_x % 8 == 0 && ((uintptr_t)x & 15) == 0 &&
+           ld_q % store_align == 0 && ((uintptr_t)q % store_align) == 0;
+}
+
+template <bool FP4>
+static void launch_quant_mx(int in_dtype, bool wide, long long blocks, hipStream_t st,
+                            const void* x, int rows, int K, int ld_x, uint8_t* q, int ld_q,
+                            uint8_t* s, int ld_s, int rule)
+{
+    const int epl = in_dtype == GA_IN_F32 ? 4 : (wide ? 8 : 4);
+    const unsigned grid = grid1d(blocks, (256 / (32 / epl)) * kQU);
+    if (in_dtype == GA_IN_F32)
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_F32, 4, FP4, kQU>), dim3(grid), dim3(256), 0, st,
+                           x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+    else if (wide)
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 8, FP4, kQU>), dim3(grid), dim3(256), 0,
+                           st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+    else
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 4, FP4, kQU>), dim3(grid), dim3(256), 0,
+                           st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+}
+
 static ga_status check_in(int in_dtype)
 {
     if (in_dtype != GA_IN_F32 && in_dtype != GA_IN_BF16)
@@ -322,9 +452,9 @@ ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x,
     if (K % 32 || ld_x % 4 || ld_q % 4)
         return fail(GA_ERR_SHAPE, "quant_mxfp8: K %% 32, ld_x %% 4 and ld_q %% 4 must be 0");
     long long blocks = (long long)rows * (K / 32);
-    GA_DISPATCH_IN(in_dtype, quant_mx_kernel, dim3(grid1d(blocks, 32)), dim3(256), 0,
-                   (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q, (uint8_t*)scales,
-                   ld_s, scale_rule);
+    launch_quant_mx<false>(in_dtype, bf16_wide(in_dtype, x, ld_x, q, ld_q, 8), blocks,
+                           (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q,
+                           (uint8_t*)scales, ld_s, scale_rule);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
 }
@@ -340,9 +470,9 @@ ga_status ga_quant_mxfp4(const void* x, int in_dtype, int rows, int K, int ld_x,
     if (K % 32 || ld_x % 4 || ld_q % 2)
         return fail(GA_ERR_SHAPE, "quant_mxfp4: K %% 32, ld_x %% 4 and ld_q %% 2 must be 0");
     long long blocks = (long long)rows * (K / 32);
-    GA_DISPATCH_IN(in_dtype, quant_mx4_kernel, dim3(grid1d(blocks, 32)), dim3(256), 0,
-                   (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q, (uint8_t*)scales,
-                   ld_s, scale_rule);
+    launch_quant_mx<true>(in_dtype, bf16_wide(in_dtype, x, ld_x, q, ld_q, 4), blocks,
+                          (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q,
+                          (uint8_t*)scales, ld_s, scale_rule);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
 }
@@ -357,8 +487,17 @@ ga_status ga_quant_fp8_1x128(const void* x, int in_dtype, int rows, int K, int l
     if (K % 128 || ld_x % 4 || ld_q % 4)
         return fail(GA_ERR_SHAPE, "quant_fp8_1x128: K %% 128, ld_x %% 4 and ld_q %% 4 must be 0");
     long long blocks = (long long)rows * (K / 128);
-    GA_DISPATCH_IN(in_dtype, quant_1x128_kernel, dim3(grid1d(blocks, 8)), dim3(256), 0,
-                   (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q, sfa, ld_s);
+    hipStream_t st = (hipStream_t)stream;
+    if (in_dtype == GA_IN_F32)
+        hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_F32, 4, kQU>), dim3(grid1d(blocks, 8 * kQU)),
+                           dim3(256), 0, st, x, rows, K, ld_x, (uint8_t*)q, ld_q, sfa, ld_s);
+    else if (bf16_wide(in_dtype, x, ld_x, q, ld_q, 8))
+        hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_BF16, 8, kQU>),
+                           dim3(grid1d(blocks, 16 * kQU)), dim3(256), 0, st, x, rows, K, ld_x,
+                           (uint8_t*)q, ld_q, sfa, ld_s);
+    else
+        hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_BF16, 4, kQU>), dim3(grid1d(blocks, 8 * kQU)),
+                           dim3(256), 0, st, x, rows, K, ld_x, (uint8_t*)q, ld_q, sfa, ld_s);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
 }
@@ -373,8 +512,16 @@ ga_status ga_quant_fp8_128x128(const void* x, int in_dtype, int rows, int K, int
     if (K % 128 || ld_x % 4 || ld_q % 4)
         return fail(GA_ERR_SHAPE, "quant_fp8_128x128: K %% 128, ld_x %% 4 and ld_q %% 4 must be 0");
     dim3 grid(K / 128, (rows + 127) / 128);
-    GA_DISPATCH_IN(in_dtype, quant_128x128_kernel, grid, dim3(256), 0, (hipStream_t)stream, x,
-                   rows, K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
+    hipStream_t st = (hipStream_t)stream;
+    if (in_dtype == GA_IN_F32)
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_F32, 4>), grid, dim3(256), 0, st, x, rows,
+                           K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
+    else if (bf16_wide(in_dtype, x, ld_x, q, ld_q, 8))
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 8>), grid, dim3(256), 0, st, x, rows,
+                           K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
+    else
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 4>), grid, dim3(256), 0, st, x, rows,
+                           K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
 }

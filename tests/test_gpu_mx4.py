@@ -172,6 +172,34 @@ def test_quant_mxfp4_bit_exact(dev, rule, in_dtype):
     np.testing.assert_array_equal(q.cpu().numpy(), wq)
 
 
+def test_e2m1_encoder_every_bf16_value(dev):
+    """Every 1x32 block holds 6.0 and 31 test values, so its scale exponent is 0
+    (rule 0: floor(log2(amax/6))) and each code is e2m1(x) itself: every bf16
+    bit pattern of magnitude <= 6 (and every NaN) goes through the device
+    encoder and is compared with the oracle's."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = oracle.bf16_bits_to_f32(bits)
+    keep = np.isnan(vals) | (np.abs(vals) <= 6.0)
+    v = vals[keep]
+    nblk = (v.size + 30) // 31
+    v = np.concatenate([v, np.zeros(nblk * 31 - v.size, np.float32)]).reshape(nblk, 31)
+    x = np.concatenate([np.full((nblk, 1), 6.0, np.float32), v], axis=1)
+    rows = 64
+    nb = (nblk + rows - 1) // rows
+    xp = np.zeros((rows * nb, 32), np.float32)
+    xp[:, 0] = 6.0
+    xp[:nblk] = x
+    x = np.ascontiguousarray(xp.reshape(rows, nb * 32))
+    for t in (torch.from_numpy(x).to(dev),
+              torch.from_numpy(oracle.to_bf16_bits(x).view(np.int16)).to(dev).view(torch.bfloat16)):
+        q, s = ops.quant_mxfp4(t, scale_rule=0)
+        torch.cuda.synchronize()
+        wq, ws = oracle.quant_mxfp4(x, 0)
+        assert (ws == 127).all()
+        np.testing.assert_array_equal(s.cpu().numpy(), ws)
+        np.testing.assert_array_equal(q.cpu().numpy(), wq)
+
+
 def test_mxfp4_gemm_one_call(dev):
     """ops.mxfp4_gemm (device quantiser, device shuffles, heuristic over the MXFP4
     manifest) against the oracle on the codes the device produced."""

@@ -70,6 +70,65 @@ def test_quant_1x128_128x128_per_tensor(dev, in_bf16):
     np.testing.assert_array_equal(q3.cpu().numpy(), o3)
 
 
+@pytest.mark.parametrize("in_bf16", [False, True])
+def test_quant_strided_rows_and_tails(dev, in_bf16):
+    """Rows whose stride is a multiple of 4 but not 8 elements (bf16 takes the
+    8-byte load path), a block count that leaves a partial last workgroup, and a
+    per-tensor size with n % 4 != 0."""
+    rows, K = 97, 1152
+    base = oracle.gen_mx_input(rows, K + 4, 55, 1.0, 6)
+    x = np.ascontiguousarray(base[:, :K])
+    if in_bf16:
+        bb = oracle.to_bf16_bits(base)
+        x = oracle.bf16_bits_to_f32(np.ascontiguousarray(bb[:, :K]))
+        xt = torch.from_numpy(bb.view(np.int16)).to(dev).view(torch.bfloat16)[:, :K]
+    else:
+        xt = torch.from_numpy(base).to(dev)[:, :K]
+    assert xt.stride(0) == K + 4
+    q, s = ops.quant_mxfp8(xt, 0)
+    q4, s4 = ops.quant_mxfp4(xt, 2)
+    q1, s1 = ops.quant_fp8_1x128(xt)
+    q2, s2 = ops.quant_fp8_128x128(xt)
+    torch.cuda.synchronize()
+    qo, so = oracle.quant_mxfp8(x, 0)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    q4o, s4o = oracle.quant_mxfp4(x, 2)
+    np.testing.assert_array_equal(s4.cpu().numpy(), s4o)
+    np.testing.assert_array_equal(q4.cpu().numpy(), q4o)
+    o1, os1 = oracle.quant_fp8_1x128(x)
+    np.testing.assert_array_equal(s1.cpu().numpy().view(np.uint32), os1.view(np.uint32))
+    np.testing.assert_array_equal(q1.cpu().numpy(), o1)
+    o2, os2 = oracle.quant_fp8_128x128(x)
+    np.testing.assert_array_equal(s2.cpu().numpy().view(np.uint32), os2.view(np.uint32))
+    np.testing.assert_array_equal(q2.cpu().numpy(), o2)
+    flat = x.reshape(-1)[:12345]
+    ft = xt.contiguous().reshape(-1)[:12345]
+    q3, s3 = ops.quant_fp8_per_tensor(ft)
+    torch.cuda.synchronize()
+    o3, os3 = oracle.quant_fp8_per_tensor(flat)
+    np.testing.assert_array_equal(s3.cpu().numpy().view(np.uint32), os3.view(np.uint32))
+    np.testing.assert_array_equal(q3.cpu().numpy(), o3)
+
+
+def test_e4m3_encoder_every_bf16_value(dev):
+    """Per-tensor quantisation with amax = 448 has scale 1, so q = e4m3(x): every
+    bf16 bit pattern of magnitude <= 448 (and every NaN) goes through the
+    device encoder and is compared with the oracle's."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = oracle.bf16_bits_to_f32(bits)
+    keep = np.isnan(vals) | (np.abs(vals) <= 448.0)
+    xb = bits[keep]
+    xb = np.concatenate([xb, oracle.to_bf16_bits(np.array([448.0], np.float32))])
+    x = oracle.bf16_bits_to_f32(xb)
+    for t in (torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16),
+              torch.from_numpy(np.ascontiguousarray(x)).to(dev)):
+        q, s = ops.quant_fp8_per_tensor(t)
+        torch.cuda.synchronize()
+        assert s.cpu().numpy()[0] == np.float32(1.0)
+        np.testing.assert_array_equal(q.cpu().numpy(), oracle.e4m3_encode(x))
+
+
 @pytest.mark.parametrize("NK", [(16, 32), (256, 512), (272, 4096)])
 def test_device_shuffle_weight(dev, NK):
     N, Kp = NK
