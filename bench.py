@@ -17,6 +17,9 @@ and M=16, N=8192, K=28672 with weights from N(0, 0.02), rotating 3 weight sets
 (the reference's own f4gemm kernels are MXFP4; its published 8192^3 figure,
 asm_f4gemm/README.md:171, is reported next to ours).
 
+"quantisers" reports the HBM bandwidth of the GPU quantisers (MX 1x32 E4M3 and
+e2m1, DeepSeek 1x128 and 128x128) on an 8192x8192 fp32 and bf16 input.
+
 "blockscale" times the DeepSeek-style GEMM (1x128 activation / 128x128 weight
 fp32 scales, fp32 C, opus_gemm kargs) at 8192^3 next to the reference's own
 published number for it (opus_gemm/block_scale_gemm/README.md:114), and the
@@ -160,6 +163,50 @@ def mfma_ceiling(torch, codes):
 
 REF_BLOCKSCALE_8192_TFLOPS = 2710.24  # opus_gemm/block_scale_gemm/README.md:114 (MI355X)
 REF_MXFP4_8192_TFLOPS = 4245.0         # asm_f4gemm/README.md:171 (MI355X, aiter code objects)
+
+
+def quant_legs(torch, steps, warmup):
+    """The GPU quantisers (HBM-bound) on an 8192x8192 activation, fp32 and bf16
+    input: algorithmic bytes (input read once, codes and scales written once)
+    per average launch, launched straight through the C ABI on preallocated
+    buffers."""
+    from gcnasm_amd import _lib
+    lib = _lib.lib()
+    n = 8192
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    q8 = torch.empty((n, n), dtype=torch.uint8, device=dev)
+    q4 = torch.empty((n, n // 2), dtype=torch.uint8, device=dev)
+    s32 = torch.empty((n, n // 32), dtype=torch.uint8, device=dev)
+    sfa = torch.empty((n // 128, n), dtype=torch.float32, device=dev)
+    sfb = torch.empty((n // 128, n // 128), dtype=torch.float32, device=dev)
+    out = []
+    for dt, code, eb in ((torch.float32, _lib.GA_IN_F32, 4), (torch.bfloat16, _lib.GA_IN_BF16, 2)):
+        x = torch.randn((n, n), device=dev).to(dt)
+        legs = (("mxfp8", lambda: lib.ga_quant_mxfp8(x.data_ptr(), code, n, n, n, q8.data_ptr(), n,
+                                                     s32.data_ptr(), n // 32, 0, sh),
+                 n * n * (eb + 1 + 1 / 32)),
+                ("mxfp4", lambda: lib.ga_quant_mxfp4(x.data_ptr(), code, n, n, n, q4.data_ptr(),
+                                                     n // 2, s32.data_ptr(), n // 32, 0, sh),
+                 n * n * (eb + 0.5 + 1 / 32)),
+                ("fp8_1x128", lambda: lib.ga_quant_fp8_1x128(x.data_ptr(), code, n, n, n,
+                                                             q8.data_ptr(), n, sfa.data_ptr(), n, sh),
+                 n * n * (eb + 1 + 4 / 128)),
+                ("fp8_128x128", lambda: lib.ga_quant_fp8_128x128(x.data_ptr(), code, n, n, n,
+                                                                 q8.data_ptr(), n, sfb.data_ptr(),
+                                                                 n // 128, sh),
+                 n * n * (eb + 1)))
+        for name, fn, nbytes in legs:
+            us = time_call(torch, lambda: _lib.check(fn()), steps, warmup)
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out.append({"workload": "quant_%s_%dx%d_%s" % (name, n, n, "f32" if eb == 4 else "bf16"),
+                        "value": round(gbs, 1), "unit": "GB/s", "kernel_avg_us": round(us, 2),
+                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(nbytes)})
+        del x
+    del q8, q4, s32, sfa, sfb
+    torch.cuda.empty_cache()
+    return out
 
 
 def mxfp4_legs(torch, ops, f4gemm, steps, warmup):
@@ -331,6 +378,7 @@ def main():
 
     blockscale, per_tensor = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
     mxfp4, mxfp4_decode = mxfp4_legs(torch, ops, f4gemm, 20, 5)
+    quant = quant_legs(torch, 20, 5)
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
@@ -360,6 +408,7 @@ def main():
         "per_tensor": per_tensor,
         "mxfp4": mxfp4,
         "mxfp4_decode": mxfp4_decode,
+        "quantisers": quant,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
