@@ -25,6 +25,10 @@ fp32 scales, fp32 C, opus_gemm kargs) at 8192^3 next to the reference's own
 published number for it (opus_gemm/block_scale_gemm/README.md:114), and the
 per-tensor fp8_gemm at 8192^3 (bf16 C).
 
+"a16w16_splitk" times the bf16 split-K GEMM + reduce (the reference's
+opus_gemm_mem_gemm_a2a driver, without its all-to-all) at the driver's default
+shape 1024x512x7168, split_k 2, and at other split counts.
+
 "mfma_ceiling" is the rate of the scaled-MFMA instruction alone (no memory
 traffic) on the 8192^3 problem's own A operand bytes, with the shader clock it
 ran at (libgcnasm_probe.so): the power-limited ceiling for this data.
@@ -255,6 +259,55 @@ def time_call(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+
+
+def a16w16_leg(torch, steps, warmup):
+    """bf16 split-K GEMM + reduce at the reference driver's default shape
+    (opus_gemm_mem_gemm_a2a/main.cc:133-136: M, N, K = 1024, 512, 7168,
+    split_k 2) and at other split counts. 'resident' reuses one input set as
+    the reference's timing loop does (its 22 MB stay in the Infinity Cache);
+    'rotating' cycles 12 sets (264 MB) so every call reads from HBM."""
+    from gcnasm_amd import flatmm_splitk as fs
+    M, N, K = 1024, 512, 7168
+    flops = 2.0 * M * N * K
+    nbytes = 2.0 * (M * K + N * K) + 2.0 * M * N
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    nsets = 12
+    sets = [(torch.randn((M, K), device="cuda:0", generator=g).to(torch.bfloat16),
+             torch.randn((N, K), device="cuda:0", generator=g).to(torch.bfloat16))
+            for _ in range(nsets)]
+    c = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0")
+    res = []
+    with fs.WorkspaceHandle() as h:
+        for split_k in (2, 1, 4, 8):
+            kas = [fs.make_kargs(a, b, c, split_k, h) for a, b in sets]
+            h.reserve(fs.workspace_bytes(kas[0]))
+            us_res = time_call(torch, lambda: fs.gemm_a16w16_splitk(kas[0]), steps, warmup)
+            it = [0]
+
+            def rot():
+                fs.gemm_a16w16_splitk(kas[it[0] % nsets])
+                it[0] += 1
+            us_rot = time_call(torch, rot, max(steps, 2 * nsets), warmup)
+            res.append({"split_k": split_k,
+                        "rotating_us": round(us_rot, 2),
+                        "rotating_tflops": round(flops / us_rot / 1e6, 1),
+                        "rotating_gbs": round(nbytes / us_rot / 1e3, 1),
+                        "resident_us": round(us_res, 2),
+                        "resident_tflops": round(flops / us_res / 1e6, 1)})
+    del sets, c
+    torch.cuda.empty_cache()
+    best = res[0]
+    return {"workload": "bf16_splitk_gemm_1024x512x7168_splitk2_plus_reduce",
+            "value": best["rotating_tflops"], "unit": "TFLOP/s",
+            "gbs": best["rotating_gbs"], "algorithmic_bytes": int(nbytes),
+            "frac_bf16_peak": round(best["rotating_tflops"] / BF16_PEAK_TFLOPS, 4),
+            "frac_hbm": round(best["rotating_gbs"] / HBM_PEAK_GBS, 4),
+            "by_split_k": res}
+
+
 def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
     """DeepSeek block-scale (fp32 C) and per-tensor (bf16 C) GEMMs at 8192^3."""
     n = 8192
@@ -385,6 +438,7 @@ def main():
     quant = quant_legs(torch, 20, 5)
     blockscale, per_tensor = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
     mxfp4 = mxfp4_leg(torch, ops, f4gemm, 20, 5)
+    a16w16 = a16w16_leg(torch, 50, 10)
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
@@ -415,6 +469,7 @@ def main():
         "mxfp4": mxfp4,
         "mxfp4_decode": mxfp4_decode,
         "quantisers": quant,
+        "a16w16_splitk": a16w16,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)

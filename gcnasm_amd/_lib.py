@@ -134,8 +134,32 @@ class MxShape(ctypes.Structure):
                  "scale_a_rows", "scale_b_rows", "d_rows_pad"]]
 
 
+class SplitkWsHandle(ctypes.Structure):
+    """opus_splitk_ws_handle (opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/gfx950/
+    opus_gemm_traits_a16w16_gfx950.cuh:588-597)."""
+
+    _fields_ = [("ptr", ctypes.c_void_p), ("bytes", ctypes.c_uint64)]
+
+
+class FlatmmSplitkKargs(ctypes.Structure):
+    """opus_gemm_flatmm_splitk_kargs_gfx950 (opus_gemm_traits_a16w16_gfx950.cuh:599-634)."""
+
+    _fields_ = [
+        ("ptr_a", ctypes.c_void_p),
+        ("ptr_b", ctypes.c_void_p),
+        ("ws_handle", ctypes.c_void_p),
+        ("ptr_c", ctypes.c_void_p),
+        ("ptr_bias", ctypes.c_void_p),
+    ] + [(n, ctypes.c_int) for n in
+         ["m", "n", "k", "batch", "split_k", "stride_a", "stride_b", "stride_ws", "stride_c",
+          "stride_a_batch", "stride_b_batch", "stride_ws_batch", "stride_c_batch",
+          "stride_bias_batch"]]
+
+
 assert ctypes.sizeof(OpusGemmKargs) == 96
 assert ctypes.sizeof(F4gemmKargs) == 0x174
+assert ctypes.sizeof(SplitkWsHandle) == 16
+assert ctypes.sizeof(FlatmmSplitkKargs) == 96
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -181,6 +205,15 @@ SIGNATURES = {
     "ga_gemm_a8w8_blockscale": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _i, _vp]),
     "ga_fp8_gemm_per_tensor": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _vp]),
     "ga_splitk_reduce": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp]),
+    "ga_splitk_reduce_ws_handle": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _i,
+                                        _vp]),
+    "ga_gemm_a16w16_flatmm_splitk": (_i, [ctypes.POINTER(FlatmmSplitkKargs), _vp]),
+    "ga_gemm_a16w16_splitk": (_i, [ctypes.POINTER(FlatmmSplitkKargs), _vp]),
+    "ga_a16w16_splitk_workspace_bytes": (_sz, [ctypes.POINTER(FlatmmSplitkKargs)]),
+    "ga_ws_handle_create": (_i, [ctypes.POINTER(_vp)]),
+    "ga_ws_handle_reserve": (_i, [_vp, _sz]),
+    "ga_ws_handle_query": (_i, [_vp, ctypes.POINTER(_vp), ctypes.POINTER(_sz)]),
+    "ga_ws_handle_destroy": (_i, [_vp]),
     "ga_device_num_cu": (_i, [ctypes.POINTER(_i)]),
 }
 

@@ -124,6 +124,16 @@ __device__ __forceinline__ v4f mfma_mx16_fp4(v8i a, v8i b, v4f c, int sa, int sb
                                                             sb);
 }
 
+// D = A(16x32) * B(32x16) + C with bf16 operands: lane l = 16*g + r holds
+// row r, K [8g, 8g+8) (16 bytes). Output as above: lane l holds
+// D[4*(l/16) + j][l%16].
+typedef __bf16 v8bf16 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v4f mfma_bf16_16x16x32(v4i a, v4i b, v4f c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf16, a),
+                                                   __builtin_bit_cast(v8bf16, b), c, 0, 0, 0);
+}
+
 // The last 16 bytes of a fragment moved to its first 16 (the fp4 operand
 // of the second 128-K half).
 __device__ __forceinline__ v8i hi16(v8i x)

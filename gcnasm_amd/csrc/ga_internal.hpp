@@ -64,19 +64,24 @@ ga_status default_workspace(size_t bytes, void** ptr);
 
 // Split-K reduce with the MX epilogue folded in:
 //   out[b, m, n] = alpha * sum_s ws[s, b, m, n] (+ bias[n]) (+ beta * c_in[b, m, n])
-// ws is [split_k, batch, padded_M, padded_N]; out/c_in rows are `ldc` elements
-// apart and batches `c_batch_stride` elements apart.
+// ws[s, b, m, n] is at (s * batch + b) * ws_batch + m * ws_ld + n; out/c_in
+// rows are `ldc` elements apart and batches `c_batch_stride` elements apart.
+// With `wsh` set, ws is read from that device slot at kernel entry (and
+// nothing is written when the slot's bytes are short of the layout).
 struct ReduceArgs {
     const float* ws;
+    const ga_splitk_ws_handle* wsh;
     void* out;
     const void* c_in;  // bf16, may be null
     const void* bias;  // may be null
     int out_dtype;
     int bias_dtype;
-    int split_k, M, N, batch, padded_M, padded_N, ldc;
+    int split_k, M, N, batch, ldc;
+    long long ws_ld, ws_batch;
     long long c_batch_stride;
     int bias_stride_batch;
     float alpha, beta;
+    int tpr_log2;  // threads per output row (set by splitk_reduce_launch)
 };
 ga_status splitk_reduce_launch(const ReduceArgs& a, hipStream_t stream);
 

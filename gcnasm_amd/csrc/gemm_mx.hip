@@ -482,6 +482,7 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
     if (gdz > 1) {
         ReduceArgs r;
         r.ws = ws;
+        r.wsh = nullptr;
         r.out = args->ptr_D;
         r.c_in = (args->beta != 0.0f) ? args->ptr_C : nullptr;
         r.bias = nullptr;
@@ -491,8 +492,8 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         r.M = M;
         r.N = N;
         r.batch = 1;
-        r.padded_M = M;
-        r.padded_N = N;
+        r.ws_ld = N;
+        r.ws_batch = (long long)M * N;
         r.ldc = (int)args->stride_C0;
         r.c_batch_stride = 0;
         r.bias_stride_batch = 0;

@@ -22,6 +22,9 @@
  *   f4gemm::shuffle_weight_16x16    asm_f4gemm/f4gemm_ref.hpp:81-96
  *   f4gemm::shuffle_scale           asm_f4gemm/f4gemm_ref.hpp:108-130
  *   splitk_reduce_kernel            opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/gfx950/splitk_reduce_gfx950.cuh:68-259
+ *   opus_splitk_ws_handle           opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/gfx950/opus_gemm_traits_a16w16_gfx950.cuh:588-597
+ *   opus_gemm_flatmm_splitk_kargs_gfx950  (same file):599-634
+ *   gemm_a16w16_flatmm_splitk_kernel opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/gfx950/opus_gemm_pipeline_a16w16_flatmm_splitk_gfx950.cuh:204-563
  */
 #ifndef GCNASM_AMD_H
 #define GCNASM_AMD_H
@@ -118,6 +121,46 @@ typedef struct ga_f4gemm_kargs {
     int log2_k_split;
 } ga_f4gemm_kargs;
 #pragma pack(pop)
+
+/* opus_splitk_ws_handle, 16 bytes: the device-resident slot through which
+ * the split-K kernels find their fp32 workspace. Kernels read it at entry,
+ * so a captured HIP graph (which holds the slot's address) still sees a
+ * workspace that was grown and moved after capture.
+ * Replaces opus_gemm_dist/.../gfx950/opus_gemm_traits_a16w16_gfx950.cuh:588-597. */
+typedef struct ga_splitk_ws_handle {
+    void* ptr;       /* current workspace; NULL until the first reserve */
+    uint64_t bytes;  /* its capacity in bytes                           */
+} ga_splitk_ws_handle;
+
+/* opus_gemm_flatmm_splitk_kargs_gfx950, 96 bytes: ptr_a@0 ptr_b@8
+ * ws_handle@16 ptr_c@24 ptr_bias@32 m@40 n@44 k@48 batch@52 split_k@56
+ * stride_a@60 stride_b@64 stride_ws@68 stride_c@72 stride_a_batch@76
+ * stride_b_batch@80 stride_ws_batch@84 stride_c_batch@88
+ * stride_bias_batch@92. Strides in elements. The workspace is fp32
+ * [split_k, batch, padded_M, padded_N]: stride_ws = padded_N,
+ * stride_ws_batch = padded_M * padded_N.
+ * Replaces opus_gemm_dist/.../gfx950/opus_gemm_traits_a16w16_gfx950.cuh:599-634. */
+typedef struct ga_flatmm_splitk_kargs {
+    const void* ptr_a;                    /* bf16 [batch, M, K]            */
+    const void* ptr_b;                    /* bf16 [batch, N, K]            */
+    const ga_splitk_ws_handle* ws_handle; /* device address of the slot    */
+    void* ptr_c;                          /* bf16 [batch, M, N]            */
+    const void* ptr_bias;                 /* bf16 [N] or [batch, N]; NULL  */
+    int m;
+    int n;
+    int k;
+    int batch;
+    int split_k;
+    int stride_a;
+    int stride_b;
+    int stride_ws;
+    int stride_c;
+    int stride_a_batch;
+    int stride_b_batch;
+    int stride_ws_batch;
+    int stride_c_batch;
+    int stride_bias_batch; /* 0: one [N] bias for all batches; N: [batch, N] */
+} ga_flatmm_splitk_kargs;
 
 /* ------------------------------------------------------------------------- */
 /* Tile manifest (f4gemm::Config, asm_f4gemm/f4gemm.hpp:120-128).            */
@@ -327,6 +370,55 @@ ga_status ga_splitk_reduce(const float* ws, void* c_out, int out_dtype, int spli
                            int M, int N, int batch, int padded_M, int padded_N,
                            const void* bias, int bias_dtype, int bias_stride_batch,
                            void* stream);
+
+/* splitk_reduce_kernel as the reference launches it: the workspace is found
+ * through the device slot `ws_handle` at kernel entry (graph-capture safe).
+ * Reads that would pass the slot's `bytes` are not made: the kernel then
+ * writes nothing. Otherwise as ga_splitk_reduce.
+ * Replaces splitk_reduce_gfx950.cuh:68-259 with its handle argument. */
+ga_status ga_splitk_reduce_ws_handle(const ga_splitk_ws_handle* ws_handle, void* c_out,
+                                     int out_dtype, int split_k, int M, int N, int batch,
+                                     int padded_M, int padded_N, const void* bias,
+                                     int bias_dtype, int bias_stride_batch, void* stream);
+
+/* gemm_a16w16_flatmm_splitk_kernel (opus_gemm_dist/opus_gemm_mem_gemm_a2a,
+ * pipeline .cuh:204-563; launch main.cc:298-300): bf16 A [batch, M, K] times
+ * bf16 B [batch, N, K]^T, K split into split_k slices; slice s writes its
+ * fp32 partial to workspace[s, b, m, n] (found through kargs->ws_handle).
+ * Slices follow the reference's partition: K in 128-element iterations,
+ * ceil(iters / split_k) per slice, the last slice takes the remainder; a
+ * slice left empty writes zeros (the reference writes nothing there).
+ * Requirements: M, N, K, batch, split_k > 0; K % 8 == 0; stride_a and
+ * stride_b >= K and multiples of 8; ptr_a / ptr_b 16-byte aligned;
+ * stride_ws >= N; stride_ws_batch >= M * stride_ws. The workspace must hold
+ * split_k * batch * stride_ws_batch floats (checked in the kernel against
+ * the slot's bytes: a slot too small makes it write nothing). ptr_c, ptr_bias
+ * are not read here. */
+ga_status ga_gemm_a16w16_flatmm_splitk(const ga_flatmm_splitk_kargs* kargs, void* stream);
+
+/* The reference's launch_once pair (main.cc:298-318): the split-K kernel,
+ * then the reduce into bf16 C with the optional bf16 bias of kargs (C rows
+ * stride_c apart, batches stride_c_batch apart). With split_k == 1 the GEMM
+ * writes C (and the bias) directly and the workspace is not touched. */
+ga_status ga_gemm_a16w16_splitk(const ga_flatmm_splitk_kargs* kargs, void* stream);
+
+/* fp32 workspace bytes the kargs' layout needs:
+ * split_k * batch * stride_ws_batch * 4. */
+size_t ga_a16w16_splitk_workspace_bytes(const ga_flatmm_splitk_kargs* kargs);
+
+/* Workspace slot management (the caller-side half of the handle protocol,
+ * which the reference leaves to its caller, main.cc:244-264):
+ *   create   allocates a device slot {NULL, 0};
+ *   reserve  makes the slot's workspace at least `bytes`: when it grows, the
+ *            device is synchronised, a new buffer is allocated, the slot is
+ *            rewritten and the old buffer is freed. Graphs captured earlier
+ *            read the new buffer on their next replay. Not capturable.
+ *   query    the slot's current {ptr, bytes} (host-side mirror);
+ *   destroy  synchronises and frees the workspace and the slot. */
+ga_status ga_ws_handle_create(ga_splitk_ws_handle** ws_handle);
+ga_status ga_ws_handle_reserve(ga_splitk_ws_handle* ws_handle, size_t bytes);
+ga_status ga_ws_handle_query(const ga_splitk_ws_handle* ws_handle, void** ptr, size_t* bytes);
+ga_status ga_ws_handle_destroy(ga_splitk_ws_handle* ws_handle);
 
 /* Device count of compute units of the current device (hipDeviceProp). */
 ga_status ga_device_num_cu(int* num_cu);

@@ -60,6 +60,8 @@ _SIGS = {
     "or_gemm_blockscale_exact": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i]),
     "or_gemm_per_tensor_fp32acc": (None, [_vp, _vp, _f, _f, _vp, _i, _i, _i]),
     "or_splitk_reduce": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i]),
+    "or_a16w16_slices": (None, [_i, _i, _vp, _vp]),
+    "or_a16w16_splitk_ws": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "or_randn": (None, [_vp, _sz, _u64, _f, _f]),
     "or_gen_mx_input": (None, [_vp, _i, _i, _u64, _f, _i]),
 }
@@ -383,3 +385,37 @@ def to_bf16_bits(x):
 
 def bf16_bits_to_f32(h):
     return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def a16w16_slices(K, split_k):
+    """[(kb, ke)] per slice of the bf16 split-K GEMM (kb == ke: empty)."""
+    kb = np.empty(split_k, np.int32)
+    ke = np.empty(split_k, np.int32)
+    load().or_a16w16_slices(K, split_k, p(kb), p(ke))
+    return list(zip(kb.tolist(), ke.tolist()))
+
+
+def a16w16_splitk_ws(a_bits, b_bits, split_k):
+    """a_bits [M, K], b_bits [N, K] (uint16 bf16 bit patterns) -> fp32 partials
+    [split_k, M, N] in the kernel's accumulation order."""
+    a_bits = np.ascontiguousarray(a_bits, dtype=np.uint16)
+    b_bits = np.ascontiguousarray(b_bits, dtype=np.uint16)
+    M, K = a_bits.shape
+    N = b_bits.shape[0]
+    ws = np.empty((split_k, M, N), np.float32)
+    load().or_a16w16_splitk_ws(p(a_bits), p(b_bits), M, N, K, K, K, split_k, p(ws))
+    return ws
+
+
+def splitk_reduce(ws, bias=None, bias_stride_batch=0):
+    """ws [split_k, batch, M, N] fp32 -> fp32 [batch, M, N] = sum over slices in
+    slice order (+ bias [N] or [batch, N], as fp32)."""
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    split_k, batch, M, N = ws.shape
+    out = np.empty((batch, M, N), np.float32)
+    bp = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float32)
+        bp = p(bias)
+    load().or_splitk_reduce(p(ws), p(out), split_k, M, N, batch, M, N, bp, bias_stride_batch)
+    return out

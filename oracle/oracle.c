@@ -665,6 +665,63 @@ void or_splitk_reduce(const float* ws, float* out, int split_k, int M, int N, in
             }
 }
 
+/* Slices of the bf16 split-K GEMM: the reference's partition
+ * (opus_gemm_dist/opus_gemm_mem_gemm_a2a/include/gfx950/
+ * opus_gemm_pipeline_a16w16_flatmm_splitk_gfx950.cuh:234-247): K in 128-wide
+ * iterations, P = ceil(iters / split_k) per slice, the last slice takes what
+ * is left. A slice with nothing left gets kb = ke.
+ * Pinned by tests/test_oracle_a16w16.py: hand-computed slice tables and
+ * one-hot K columns that land in exactly one slice. */
+void or_a16w16_slices(int K, int split_k, int* kb, int* ke)
+{
+    int iters = (K + 127) / 128;
+    int per = (iters + split_k - 1) / split_k;
+    for (int s = 0; s < split_k; s++) {
+        long long b = (long long)s * per * 128;
+        long long e = b + (long long)per * 128;
+        if (e > K)
+            e = K;
+        if (b > K)
+            b = K;
+        kb[s] = (int)b;
+        ke[s] = (int)e;
+    }
+}
+
+/* gemm_a16w16_flatmm_splitk_kernel (pipeline .cuh:204-563): slice s of
+ * A [M, K] (row stride lda) times B [N, K]^T (ldb), both bf16 bit patterns,
+ * into ws[s, m, n] (fp32, [split_k, M, N]); an empty slice is all zeros. In a
+ * slice, the exact sum of each 32-wide K group (one bf16 MFMA) is added to
+ * the fp32 accumulator with one rounding.
+ * Pinned by tests/test_oracle_a16w16.py: integer-valued operands (exact in
+ * fp32: equals the integer product A B^T), the f64 error bound on N(0,1) data,
+ * the slice tables above, and a planted transposition. */
+void or_a16w16_splitk_ws(const uint16_t* A, const uint16_t* B, int M, int N, int K, int lda,
+                         int ldb, int split_k, float* ws)
+{
+    int* kb = (int*)malloc(sizeof(int) * (size_t)split_k);
+    int* ke = (int*)malloc(sizeof(int) * (size_t)split_k);
+    or_a16w16_slices(K, split_k, kb, ke);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int s = 0; s < split_k; s++)
+            for (int j = 0; j < N; j++) {
+                const uint16_t* a = A + (size_t)i * lda;
+                const uint16_t* b = B + (size_t)j * ldb;
+                float acc = 0.0f;
+                for (int k = kb[s]; k < ke[s]; k += 32) {
+                    int e = k + 32 < ke[s] ? k + 32 : ke[s];
+                    long double g = 0.0L;
+                    for (int t = k; t < e; t++)
+                        g += (long double)or_bf16_to_f32(a[t]) * (long double)or_bf16_to_f32(b[t]);
+                    acc = (float)((long double)acc + g);
+                }
+                ws[((size_t)s * M + i) * N + j] = acc;
+            }
+    free(kb);
+    free(ke);
+}
+
 /* ------------------------------------------------------------------------- */
 /* Synthetic inputs                                                           */
 /* ------------------------------------------------------------------------- */

@@ -117,6 +117,13 @@ void or_gemm_per_tensor_fp32acc(const uint8_t* A, const uint8_t* B, float sa, fl
 void or_splitk_reduce(const float* ws, float* out, int split_k, int M, int N, int batch,
                       int padded_M, int padded_N, const float* bias, int bias_stride_batch);
 
+/* bf16 split-K GEMM (opus_gemm_dist/opus_gemm_mem_gemm_a2a, pipeline
+ * .cuh:234-247 partition, :204-563 kernel): slice bounds, and the fp32
+ * partials ws [split_k, M, N] (per 32-K group: exact sum, one fp32 rounding). */
+void or_a16w16_slices(int K, int split_k, int* kb, int* ke);
+void or_a16w16_splitk_ws(const uint16_t* A, const uint16_t* B, int M, int N, int K, int lda,
+                         int ldb, int split_k, float* ws);
+
 /* ---- synthetic inputs ---------------------------------------------------- */
 /* Deterministic stream: splitmix64. Normal samples by Box-Muller on f64. */
 void or_randn(float* out, size_t n, uint64_t seed, float mean, float std);

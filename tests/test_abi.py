@@ -80,3 +80,55 @@ def test_mx_launch_validation_without_gpu():
     assert l.ga_kernel_launch(0, ctypes.byref(args), 99, 1, 1, None, 0, None) == _lib.GA_ERR_ARG
     l.ga_fill_args(ctypes.byref(args), 8, None, 8, 8, 8, 8, 64, 60, 256, 64, 8, 8, 1.0, 0.0, 0)
     assert l.ga_kernel_launch(0, ctypes.byref(args), 1, 1, 1, None, 0, None) == _lib.GA_ERR_SHAPE
+
+
+def test_flatmm_splitk_structs_match_reference_layout():
+    """opus_splitk_ws_handle / opus_gemm_flatmm_splitk_kargs_gfx950 byte layout
+    (opus_gemm_traits_a16w16_gfx950.cuh:588-634)."""
+    K = _lib.FlatmmSplitkKargs
+    assert ctypes.sizeof(_lib.SplitkWsHandle) == 16
+    assert ctypes.sizeof(K) == 96
+    want = dict(ptr_a=0, ptr_b=8, ws_handle=16, ptr_c=24, ptr_bias=32, m=40, n=44, k=48,
+                batch=52, split_k=56, stride_a=60, stride_b=64, stride_ws=68, stride_c=72,
+                stride_a_batch=76, stride_b_batch=80, stride_ws_batch=84, stride_c_batch=88,
+                stride_bias_batch=92)
+    for name, off in want.items():
+        assert getattr(K, name).offset == off, name
+
+
+def test_flatmm_splitk_validation_without_gpu():
+    l = _lib.lib()
+    assert l.ga_gemm_a16w16_flatmm_splitk(None, None) == _lib.GA_ERR_ARG
+    assert l.ga_gemm_a16w16_splitk(None, None) == _lib.GA_ERR_ARG
+    ka = _lib.FlatmmSplitkKargs()
+    ka.ptr_a = ka.ptr_b = ka.ptr_c = 0x10000
+    ka.ws_handle = 0x20000
+    ka.m, ka.n, ka.k, ka.batch, ka.split_k = 64, 64, 100, 1, 2   # K % 8 != 0
+    ka.stride_a = ka.stride_b = 104
+    ka.stride_ws, ka.stride_c, ka.stride_ws_batch = 64, 64, 64 * 64
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_SHAPE
+    ka.k = 96
+    ka.stride_a = 90                                              # < K
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_SHAPE
+    ka.stride_a = 96
+    ka.ptr_a = 0x10008                                            # not 16-byte aligned
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_ARG
+    ka.ptr_a = 0x10000
+    ka.stride_ws = 32                                             # < N
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_SHAPE
+    ka.stride_ws, ka.stride_ws_batch = 64, 63 * 64                # < M * stride_ws
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_SHAPE
+    ka.stride_ws_batch = 64 * 64
+    ka.ws_handle = None
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_ARG
+    ka.split_k = 0
+    assert l.ga_gemm_a16w16_flatmm_splitk(ctypes.byref(ka), None) == _lib.GA_ERR_ARG
+    ka.split_k, ka.batch = 3, 2
+    assert l.ga_a16w16_splitk_workspace_bytes(ctypes.byref(ka)) == 3 * 2 * 64 * 64 * 4
+    assert l.ga_splitk_reduce_ws_handle(None, None, 0, 2, 1, 1, 1, 1, 1, None, 0, 0,
+                                        None) == _lib.GA_ERR_ARG
+    # slots are only those made by ga_ws_handle_create
+    assert l.ga_ws_handle_reserve(0x1234, 64) == _lib.GA_ERR_ARG
+    assert l.ga_ws_handle_query(0x1234, None, None) == _lib.GA_ERR_ARG
+    assert l.ga_ws_handle_destroy(0x1234) == _lib.GA_ERR_ARG
+    assert l.ga_ws_handle_create(None) == _lib.GA_ERR_ARG
