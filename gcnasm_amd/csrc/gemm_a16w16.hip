@@ -7,7 +7,7 @@
 //
 // Reference: gemm_a16w16_flatmm_splitk_kernel (opus_gemm_dist/
 // opus_gemm_mem_gemm_a2a/include/gfx950/opus_gemm_pipeline_a16w16_flatmm_
-// splitk_gfx950.cuh:204-563), launched with the reduce by main.cc:298-318;
+// splitk_gfx950.cuh:204-563), launched with the reduce by main.cc:299-318;
 // kargs and handle opus_gemm_traits_a16w16_gfx950.cuh:588-634.
 //
 // Kernel design (gfx950, 256 threads = 4 waves in a 2 x 2 grid):

@@ -7,7 +7,7 @@ Mirrors the reference's a16w16 flatmm split-K path:
   opus_gemm_flatmm_splitk_kargs     (same file):599-634
   gemm_a16w16_flatmm_splitk_kernel  .../opus_gemm_pipeline_a16w16_flatmm_splitk_gfx950.cuh:204-563
   splitk_reduce_kernel              .../splitk_reduce_gfx950.cuh:68-259
-  launch_once (GEMM + reduce)       opus_gemm_dist/opus_gemm_mem_gemm_a2a/main.cc:298-318
+  launch_once (GEMM + reduce)       opus_gemm_dist/opus_gemm_mem_gemm_a2a/main.cc:299-318
 
 The workspace is reached through a device slot {ptr, bytes} that the kernels
 read at entry, so a HIP graph captured once keeps working after the slot's

@@ -382,7 +382,7 @@ ga_status ga_splitk_reduce_ws_handle(const ga_splitk_ws_handle* ws_handle, void*
                                      int bias_dtype, int bias_stride_batch, void* stream);
 
 /* gemm_a16w16_flatmm_splitk_kernel (opus_gemm_dist/opus_gemm_mem_gemm_a2a,
- * pipeline .cuh:204-563; launch main.cc:298-300): bf16 A [batch, M, K] times
+ * pipeline .cuh:204-563; launch main.cc:299-318): bf16 A [batch, M, K] times
  * bf16 B [batch, N, K]^T, K split into split_k slices; slice s writes its
  * fp32 partial to workspace[s, b, m, n] (found through kargs->ws_handle).
  * Slices follow the reference's partition: K in 128-element iterations,
@@ -396,7 +396,7 @@ ga_status ga_splitk_reduce_ws_handle(const ga_splitk_ws_handle* ws_handle, void*
  * are not read here. */
 ga_status ga_gemm_a16w16_flatmm_splitk(const ga_flatmm_splitk_kargs* kargs, void* stream);
 
-/* The reference's launch_once pair (main.cc:298-318): the split-K kernel,
+/* The reference's launch_once pair (main.cc:299-318): the split-K kernel,
  * then the reduce into bf16 C with the optional bf16 bias of kargs (C rows
  * stride_c apart, batches stride_c_batch apart). With split_k == 1 the GEMM
  * writes C (and the bias) directly and the workspace is not touched. */
