@@ -10,15 +10,16 @@
 // splitk_gfx950.cuh:204-563), launched with the reduce by main.cc:299-318;
 // kargs and handle opus_gemm_traits_a16w16_gfx950.cuh:588-634.
 //
-// Kernel design (gfx950, 256 threads = 4 waves in a 2 x 2 grid):
-//  * K step of 64 bf16 = 128 bytes per row, so the LDS image of a 16-row
-//    group is the 2 KB [16-byte chunk:8][row:16][16 B] layout of the MXFP8
-//    kernels, filled by direct-to-LDS 16-byte buffer loads; rows past M fall
-//    outside the buffer range and read as zero.
+// Kernel design (gfx950, 256 threads = 4 waves in a 2 x 2 grid, tiles from
+// 64x64 to 128x256):
+//  * K step of 64 bf16 = 128 bytes per row, kept in LDS as the 256x256 FP8
+//    kernels keep theirs: 128-byte rows with 16-byte K chunk c of row r at
+//    slot c ^ ((r >> 1) & 7), so a direct-to-LDS copy instruction fetches 8
+//    whole rows (full 128-byte lines) and the operand reads are free of bank
+//    conflicts; rows past M fall outside the buffer range and read as zero.
 //  * v_mfma_f32_16x16x32_bf16: lane 16g+r takes row r, K [8g, 8g+8), which is
-//    chunk g of the row: the first 1 KB of a group is the operand for K
-//    [0, 32) and the second 1 KB for K [32, 64), each one linear
-//    ds_read_b128 per lane (no bank conflicts).
+//    chunk g of the row (K [0, 32)); chunk g + 4 feeds the second MFMA
+//    (K [32, 64)).
 //  * Operands swapped (B rows on the MFMA's A side), so a lane ends with 4
 //    consecutive N outputs of one C row -> 16-byte fp32 stores.
 //  * Slices follow the reference's partition (pipeline .cuh:234-247): K in
@@ -34,6 +35,7 @@
 //    share A and B panels of the same K range in its L2.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
+#include "ga_pp.hpp"
 
 #include <mutex>
 #include <unordered_map>
@@ -105,19 +107,20 @@ __device__ __forceinline__ void a16_compute(const char* smem, int buf, int wm, i
 {
     const char* la = smem + buf * C::STAGE;
     const char* lb = la + C::A_BYTES;
-    const int lo = lane * 16;
+    uint32_t o0, o1;
+    pp::operand_lane(lane, o0, o1);
     v4i a[2][C::TM], b[2][C::TN];
 #pragma unroll
     for (int t = 0; t < C::TN; t++) {
-        const char* g = lb + (wn * C::TN + t) * 2048 + lo;
-        b[0][t] = *(const v4i*)g;
-        b[1][t] = *(const v4i*)(g + 1024);
+        const char* g = lb + (wn * C::TN + t) * 2048;
+        b[0][t] = *(const v4i*)(g + o0);
+        b[1][t] = *(const v4i*)(g + o1);
     }
 #pragma unroll
     for (int i = 0; i < C::TM; i++) {
-        const char* g = la + (wm * C::TM + i) * 2048 + lo;
-        a[0][i] = *(const v4i*)g;
-        a[1][i] = *(const v4i*)(g + 1024);
+        const char* g = la + (wm * C::TM + i) * 2048;
+        a[0][i] = *(const v4i*)(g + o0);
+        a[1][i] = *(const v4i*)(g + o1);
     }
     // K [0, 32) over every accumulator, then K [32, 64): no back-to-back
     // dependent MFMAs
@@ -226,18 +229,17 @@ void a16w16_splitk_kernel(A16Args p)
         const long long bbytes = (long long)(N - n0) * ldb;
         st.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
         st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
-        const int chunk = (tid & 127) >> 4;
+        // copy i covers rows 32i .. 32i+31 (wave w: 8 whole rows) of the
+        // swizzled LDS image; the lane's K chunk is the same for every i
+        int row0, chunk;
+        pp::copy_lane(wave, lane, row0, chunk);
         st.kchunk = chunk * 8;
 #pragma unroll
-        for (int i = 0; i < C::A_LOADS; i++) {
-            const int row = (2 * i + (tid >> 7)) * 16 + (tid & 15);
-            st.voff_a[i] = (uint32_t)row * lda + chunk * 16;
-        }
+        for (int i = 0; i < C::A_LOADS; i++)
+            st.voff_a[i] = (uint32_t)(i * 32 + row0) * lda + chunk * 16;
 #pragma unroll
-        for (int i = 0; i < C::B_LOADS; i++) {
-            const int row = (2 * i + (tid >> 7)) * 16 + (tid & 15);
-            st.voff_b[i] = (uint32_t)row * ldb + chunk * 16;
-        }
+        for (int i = 0; i < C::B_LOADS; i++)
+            st.voff_b[i] = (uint32_t)(i * 32 + row0) * ldb + chunk * 16;
     }
 
     v4f acc[C::TM][C::TN];
@@ -296,7 +298,7 @@ void a16w16_splitk_kernel(A16Args p)
     }
 }
 
-// Tile choice: the largest tile whose grid still covers every CU once.
+// One configuration over split_k x tiles workgroups (x) and batch (z).
 template <class C, int EPI>
 static ga_status launch_a16(const ga_flatmm_splitk_kargs& ka, int kslice, hipStream_t stream)
 {
@@ -314,7 +316,13 @@ static ga_status launch_a16(const ga_flatmm_splitk_kargs& ka, int kslice, hipStr
     return GA_OK;
 }
 
+// Tile configurations, largest first. Measured on MI355X (bf16, 2048-8192
+// sized problems and the skinny 1024x512x7168): the largest tile whose grid
+// still gives every CU a workgroup wins; 128-row tiles are not used for M up
+// to 64 (they would compute mostly padding).
+typedef A16Cfg<128, 256, 2> A16Huge;
 typedef A16Cfg<128, 128, 3> A16Big;
+typedef A16Cfg<64, 128, 4> A16Mid;
 typedef A16Cfg<64, 64, 4> A16Small;
 
 template <int EPI>
@@ -327,10 +335,16 @@ static ga_status dispatch_a16(const ga_flatmm_splitk_kargs& ka, hipStream_t stre
     const int iters = (ka.k + 127) / 128;
     const int per = (iters + ka.split_k - 1) / ka.split_k;
     const int kslice = per * 128;
-    const long long big = (long long)((ka.m + 127) / 128) * ((ka.n + 127) / 128) * ka.split_k *
-                          ka.batch;
-    if (big >= num_cu)
+    auto wgs = [&](int bm, int bn) {
+        return (long long)((ka.m + bm - 1) / bm) * ((ka.n + bn - 1) / bn) * ka.split_k * ka.batch;
+    };
+    const bool tall = ka.m > 64;
+    if (tall && wgs(128, 256) >= num_cu)
+        return launch_a16<A16Huge, EPI>(ka, kslice, stream);
+    if (tall && wgs(128, 128) >= num_cu)
         return launch_a16<A16Big, EPI>(ka, kslice, stream);
+    if (wgs(64, 128) >= num_cu)
+        return launch_a16<A16Mid, EPI>(ka, kslice, stream);
     return launch_a16<A16Small, EPI>(ka, kslice, stream);
 }
 

@@ -66,6 +66,8 @@ SHAPES = [
     (300, 40, 8, 1),        # K = 8
     (1024, 1024, 3000, 4),  # 128x128 tiles, K tail
     (2048, 1536, 1024, 2),  # 128x128 tiles
+    (2048, 2048, 1000, 2),  # 128x256 tiles, K tail
+    (520, 1000, 1024, 4),   # 64x128 tiles, ragged M and N
 ]
 
 
@@ -92,7 +94,7 @@ def test_partials(dev, shape):
     assert st["bad"] == 0
 
 
-@pytest.mark.parametrize("shape", SHAPES[:6] + [(1024, 1024, 3000, 4)])
+@pytest.mark.parametrize("shape", SHAPES[:6] + SHAPES[7:])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm(dev, shape, with_bias):
     M, N, K, split_k = shape
