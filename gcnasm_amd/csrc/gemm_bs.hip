@@ -14,12 +14,14 @@
 // C is fp32 (the reference's output type) or bf16.
 //
 // Up to 64 rows (this file): 4 waves, 64x256 tile, K step 128, A and B
-// staged with buffer_load ... lds into the MFMA-order LDS image,
+// staged with buffer_load ... lds (8 whole 128-byte rows per instruction)
+// into swizzled LDS rows (chunk c of row r at slot c ^ ((r >> 1) & 7)),
 // v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales (127) and the
 // operands swapped so a lane owns 4 consecutive N of one C row. More rows go
 // to the 256x256 eight-wave kernel of gemm_bs_pp.hip.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
+#include "ga_pp.hpp"
 
 namespace ga {
 
@@ -89,17 +91,17 @@ void bs_gemm_kernel(ga_opus_gemm_kargs ka, int tiles_n)
     const long long bbytes = (long long)(N - n0) * ka.stride_b;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+    // copy i covers rows 32i .. 32i+31 (wave w: 8 whole 128-byte rows) of the
+    // swizzled LDS image
     uint32_t voff_a[C::A_LOADS], voff_b[C::B_LOADS];
+    int row0, chunk;
+    pp::copy_lane(wave, lane, row0, chunk);
 #pragma unroll
-    for (int i = 0; i < C::A_LOADS; i++) {
-        int idx = i * 256 + tid, g = idx >> 7, u = idx & 127;
-        voff_a[i] = (uint32_t)(g * 16 + (u & 15)) * ka.stride_a + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
-    }
+    for (int i = 0; i < C::A_LOADS; i++)
+        voff_a[i] = (uint32_t)(i * 32 + row0) * ka.stride_a + chunk * 16;
 #pragma unroll
-    for (int i = 0; i < C::B_LOADS; i++) {
-        int idx = i * 256 + tid, g = idx >> 7, u = idx & 127;
-        voff_b[i] = (uint32_t)(g * 16 + (u & 15)) * ka.stride_b + (u >> 5) * 32 + ((u >> 4) & 1) * 16;
-    }
+    for (int i = 0; i < C::B_LOADS; i++)
+        voff_b[i] = (uint32_t)(i * 32 + row0) * ka.stride_b + chunk * 16;
 
     // Scale pointers for this lane's C rows / columns.
     const float* sfa = (const float*)ka.ptr_sfa + (size_t)b * ka.stride_sfa_batch;
@@ -151,20 +153,21 @@ void bs_gemm_kernel(ga_opus_gemm_kargs ka, int tiles_n)
     auto compute = [&](int buf, const BsScales<C>& s) {
         const char* la = smem + buf * C::STAGE;
         const char* lb = la + C::A_BYTES;
-        const int lo = lane * 16;
+        uint32_t o0, o1;
+        pp::operand_lane(lane, o0, o1);
         v8i bf[C::TN];
 #pragma unroll
         for (int t = 0; t < C::TN; t++) {
-            const char* g = lb + (wn * C::TN + t) * 2048 + lo;
-            v4i x0 = *(const v4i*)(g);
-            v4i x1 = *(const v4i*)(g + 1024);
+            const char* g = lb + (wn * C::TN + t) * 2048;
+            v4i x0 = *(const v4i*)(g + o0);
+            v4i x1 = *(const v4i*)(g + o1);
             bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
         }
 #pragma unroll
         for (int i = 0; i < C::TM; i++) {
-            const char* g = la + (wm * C::TM + i) * 2048 + lo;
-            v4i x0 = *(const v4i*)(g);
-            v4i x1 = *(const v4i*)(g + 1024);
+            const char* g = la + (wm * C::TM + i) * 2048;
+            v4i x0 = *(const v4i*)(g + o0);
+            v4i x1 = *(const v4i*)(g + o1);
             v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
             for (int t = 0; t < C::TN; t++) {

@@ -9,13 +9,16 @@
 //  * block tile BM x BN, K step 128; waves in a WAVES_M x WAVES_N grid, each
 //    owning (BM/WAVES_M) x (BN/WAVES_N) of C as 16x16 MFMA tiles.
 //  * A and B are staged in LDS with buffer_load ... lds (16 B per lane,
-//    out-of-range rows read as zero), two stages. The LDS image of every
-//    16-row x 128-K group is 2 KB ordered [K/16:8][row:16][16 B], which is
-//    exactly the preshuffled-B byte order, so B is a linear copy.
+//    out-of-range rows read as zero), 2-4 stages. Row-major operands (A, and
+//    B when not preshuffled) sit as 128-byte rows with 16-byte K chunk c of
+//    row r at slot c ^ ((r >> 1) & 7): each copy instruction fetches 8 whole
+//    rows (full 128-byte lines), and the operand reads are conflict-free.
+//    Preshuffled B keeps its own byte order, 2 KB per 16-row x 128-K group
+//    ordered [K/16:8][row:16][16 B], so it is a linear copy.
 //  * MFMA operand layout of v_mfma_scale_f32_16x16x128_f8f6f4 (fp8): lane
 //    l = 16*g + r holds row r; its VGPRs 0-3 carry K [16g, 16g+16) and VGPRs
-//    4-7 carry K [64+16g, 64+16g+16). So operand half h of every lane is the
-//    1 KB at LDS offset h*1024 + l*16: linear ds_read_b128, no bank conflicts.
+//    4-7 carry K [64+16g, 64+16g+16): chunks g and g + 4 of row r (for
+//    preshuffled B, the 1 KB halves at l*16 and 1024 + l*16).
 //    The E8M0 scale in lane 16*b + r applies to row r, K [32b, 32b+32).
 //  * v_mfma_scale_f32_16x16x128_f8f6f4 with operands swapped (B rows feed
 //    the MFMA's A side) so each lane ends up with 4 consecutive N outputs of
@@ -30,6 +33,7 @@
 //    tiles and shares A/B panels in its own L2.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
+#include "ga_pp.hpp"
 
 #include <cstring>
 #include <mutex>
@@ -116,6 +120,9 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
     const char* lb = la + C::A_BYTES;
     const char* ls = lb + C::B_BYTES;
     const int lo = lane * 16;
+    uint32_t o0, o1; // swizzled row-major operands
+    pp::operand_lane(lane, o0, o1);
+    const uint32_t b0 = C::BPS ? (uint32_t)lo : o0, b1 = C::BPS ? (uint32_t)lo + 1024 : o1;
     // this step's 128-K half of each scale dword moved to bytes 0-1
     const uint32_t sh = (uint32_t)(step & 1) * 16;
     uint32_t sa[C::SM], sb[C::SN];
@@ -128,16 +135,16 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
     v8i bf[C::TN];
 #pragma unroll
     for (int t = 0; t < C::TN; t++) {
-        const char* g = lb + (wn * C::TN + t) * 2048 + lo;
-        v4i x0 = *(const v4i*)(g);
-        v4i x1 = *(const v4i*)(g + 1024);
+        const char* g = lb + (wn * C::TN + t) * 2048;
+        v4i x0 = *(const v4i*)(g + b0);
+        v4i x1 = *(const v4i*)(g + b1);
         bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
     }
     static_for<C::TM>([&](auto I) {
         constexpr int i = decltype(I)::value;
-        const char* g = la + (wm * C::TM + i) * 2048 + lo;
-        v4i x0 = *(const v4i*)(g);
-        v4i x1 = *(const v4i*)(g + 1024);
+        const char* g = la + (wm * C::TM + i) * 2048;
+        v4i x0 = *(const v4i*)(g + o0);
+        v4i x1 = *(const v4i*)(g + o1);
         v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
         static_for<C::TN>([&](auto T) {
             constexpr int t = decltype(T)::value;
@@ -179,13 +186,13 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
         long long abytes = (long long)(M - m0) * lda;
         st.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+        // row-major operands: copy i covers rows 32i .. 32i+31 (wave w: 8
+        // whole 128-byte rows) of the swizzled LDS image
+        int row0, chunk;
+        pp::copy_lane(wave, lane, row0, chunk);
 #pragma unroll
-        for (int i = 0; i < C::A_LOADS; i++) {
-            int idx = i * 256 + tid;
-            int g = idx >> 7, u = idx & 127;
-            int row = g * 16 + (u & 15);
-            st.voff_a[i] = (uint32_t)row * lda + (u >> 4) * 16;
-        }
+        for (int i = 0; i < C::A_LOADS; i++)
+            st.voff_a[i] = (uint32_t)(i * 32 + row0) * lda + chunk * 16;
         if (C::BPS) {
             const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
             long long bbytes = (long long)(N - n0) * K;
@@ -203,12 +210,8 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
             st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
             st.b_kstride = 128;
 #pragma unroll
-            for (int i = 0; i < C::B_LOADS; i++) {
-                int idx = i * 256 + tid;
-                int g = idx >> 7, u = idx & 127;
-                int row = g * 16 + (u & 15);
-                st.voff_b[i] = (uint32_t)row * ldb + (u >> 4) * 16;
-            }
+            for (int i = 0; i < C::B_LOADS; i++)
+                st.voff_b[i] = (uint32_t)(i * 32 + row0) * ldb + chunk * 16;
         }
         // Scales: shuffled layout, 256-byte block per (32 rows, 256 K).
         const int sma = (M + 31) / 32 * 32, smb = (N + 31) / 32 * 32;
