@@ -53,6 +53,10 @@ ga_status device_cu_count(int* num_cu);
 // 256x256 eight-wave fp32-scaled FP8 GEMM (gemm_bs_pp.hip); mode 0 = block
 // scale GROUP_N 128, 1 = GROUP_N 1, 2 = per-tensor.
 void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStream_t stream);
+// The same GEMMs for up to 64 rows, streaming B (gemm_bs_decode.hip); same
+// mode numbering.
+ga_status launch_bs_decode(const ga_opus_gemm_kargs& ka, int mode, int out_dtype,
+                           hipStream_t stream);
 int mx_registry_count();  // MXFP8 manifest rows (registry entries [0, count))
 int mx_registry_total();  // every registry entry (manifests + kernels reachable by name)
 const MxKernel* mx_registry_get(int idx);

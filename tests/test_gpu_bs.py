@@ -49,7 +49,13 @@ def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
 @pytest.mark.parametrize("group_n", [128, 1])
 @pytest.mark.parametrize("shape", [(256, 512, 256), (384, 2112, 1024), (96, 1000, 512),
                                    (33, 7168, 512), (1, 256, 384), (520, 784, 1152),
-                                   (65, 300, 640)])
+                                   (65, 300, 640),
+                                   # up to 64 rows: the B-streaming kernel (K slices,
+                                   # ragged N, one or two column groups per wave) ...
+                                   (16, 1000, 2048), (64, 7168, 1024), (8, 3000, 1536),
+                                   (1, 8200, 4096),
+                                   # ... or the 64x256 tile when it has enough tiles
+                                   (40, 16640, 256)])
 def test_blockscale(dev, group_n, shape):
     M, N, K = shape
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + N, group_n=group_n)
@@ -83,8 +89,19 @@ def test_blockscale_batched(dev):
         assert st["bad"] == 0, b
 
 
+def test_blockscale_batched_small_m(dev):
+    M, N, K, batch = 20, 700, 1024, 3
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=9, batch=batch)
+    C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
+    for b in range(batch):
+        want = oracle.gemm_blockscale_fp32acc(qa[b], qb[b], sfa[b], sfb[b], 128)
+        absdot = oracle.blockscale_absdot(qa[b], qb[b], sfa[b], sfb[b], 128)
+        ok, st = f32_compare(C[b].cpu().numpy(), want, absdot=absdot)
+        assert st["bad"] == 0, b
+
+
 @pytest.mark.parametrize("shape", [(256, 256, 512), (200, 1040, 1024), (1, 512, 256),
-                                   (600, 1000, 768)])
+                                   (600, 1000, 768), (16, 4000, 2048), (48, 600, 1024)])
 def test_per_tensor(dev, shape):
     M, N, K = shape
     xa = oracle.randn(M * K, 11).reshape(M, K)
