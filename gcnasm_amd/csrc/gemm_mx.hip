@@ -41,11 +41,15 @@
 
 namespace ga {
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, bool BPS_, int NS_ = 2>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, bool BPS_, int NS_ = 2, bool FP4_ = false>
 struct MxCfg {
     static constexpr int BM = BM_, BN = BN_;
     static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
     static constexpr bool BPS = BPS_;
+    // MXFP4: e2m1 packed two per byte; a step is 256 K = the same 128 bytes
+    // per row, so copies and LDS layouts are the MXFP8 ones
+    static constexpr bool FP4 = FP4_;
+    static constexpr int EPB = FP4 ? 2 : 1;
     static constexpr int NS = NS_; // LDS stages in flight
     static constexpr int NT = 256;
     static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -84,9 +88,10 @@ struct MxState {
     uint32_t b_kstride;        // bytes per K step of 128 in B
 };
 
-// Direct-to-LDS copy of 128-K step `step` of the slice (global K offset kk)
-// into stage `buf`: A and B tiles, then this wave's scale blocks. The scale
-// dword covers 256 K (bytes 2*d4 + d1, d4 = step & 1, d1 = 16-row half).
+// Direct-to-LDS copy of step `step` of the slice (byte offset kk inside a
+// row, a multiple of 128) into stage `buf`: A and B tiles, then this wave's
+// scale blocks. The scale dword covers 256 K: MXFP8 steps use bytes
+// 2*d4 + d1 (d4 = step & 1, d1 = 16-row half), an MXFP4 step all four.
 template <class C>
 __device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, int buf, int step,
                                             int kk, int wave)
@@ -101,7 +106,7 @@ __device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, in
     for (int i = 0; i < C::B_LOADS; i++)
         lds_load16(st.rb, (lds_void*)(sb + (i * 256 + wave * 64) * 16),
                    st.voff_b[i] + (uint32_t)(kk / 128) * st.b_kstride, 0);
-    const uint32_t q = (uint32_t)(step >> 1) * 256;
+    const uint32_t q = (uint32_t)(C::FP4 ? step : (step >> 1)) * 256;
 #pragma unroll
     for (int i = 0; i < C::S_LOADS; i++) {
         lds_void* dst = (lds_void*)(ss + (wave * C::S_LOADS + i) * 256);
@@ -123,8 +128,8 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
     uint32_t o0, o1; // swizzled row-major operands
     pp::operand_lane(lane, o0, o1);
     const uint32_t b0 = C::BPS ? (uint32_t)lo : o0, b1 = C::BPS ? (uint32_t)lo + 1024 : o1;
-    // this step's 128-K half of each scale dword moved to bytes 0-1
-    const uint32_t sh = (uint32_t)(step & 1) * 16;
+    // MXFP8: this step's 128-K half of each scale dword moved to bytes 0-1
+    const uint32_t sh = C::FP4 ? 0u : (uint32_t)(step & 1) * 16;
     uint32_t sa[C::SM], sb[C::SN];
 #pragma unroll
     for (int t = 0; t < C::SM; t++)
@@ -149,9 +154,19 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
         static_for<C::TN>([&](auto T) {
             constexpr int t = decltype(T)::value;
             // op_sel picks the 16-row half inside the 32-row scale block; the
-            // 128-K half was selected by the caller's shift of the dword
-            acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(bf[t], af, acc[i][t], (int)sb[t >> 1],
-                                                    (int)sa[i >> 1]);
+            // 128-K half is the dword's low 16 bits (MXFP8: shifted there
+            // above; MXFP4: the first of the step's two MFMAs, the second
+            // takes the high 16 bits and the fragments' last 16 bytes)
+            if constexpr (C::FP4) {
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(bf[t], af, acc[i][t],
+                                                             (int)sb[t >> 1], (int)sa[i >> 1]);
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(hi16(bf[t]), hi16(af), acc[i][t],
+                                                             (int)(sb[t >> 1] >> 16),
+                                                             (int)(sa[i >> 1] >> 16));
+            } else {
+                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(bf[t], af, acc[i][t], (int)sb[t >> 1],
+                                                        (int)sa[i >> 1]);
+            }
         });
     });
 }
@@ -176,9 +191,10 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
     const int kb = z * kpt;
     const int ke = min(K, kb + kpt);
-    const int nsteps = (ke - kb) / 128;
+    const int nsteps = (ke - kb) / (128 * C::EPB);
+    const int kbb = kb / C::EPB, Kb = K / C::EPB; // bytes
 
-    const uint32_t lda = args.stride_A0, ldb = args.stride_B0;
+    const uint32_t lda = args.stride_A0 / C::EPB, ldb = args.stride_B0 / C::EPB; // bytes
     const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
 
     MxState<C> st;
@@ -194,15 +210,15 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         for (int i = 0; i < C::A_LOADS; i++)
             st.voff_a[i] = (uint32_t)(i * 32 + row0) * lda + chunk * 16;
         if (C::BPS) {
-            const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * K * 16;
-            long long bbytes = (long long)(N - n0) * K;
+            const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * Kb * 16;
+            long long bbytes = (long long)(N - n0) * Kb;
             st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
             st.b_kstride = 128 * 16;
 #pragma unroll
             for (int i = 0; i < C::B_LOADS; i++) {
                 int idx = i * 256 + tid;
                 int g = idx >> 7, u = idx & 127;
-                st.voff_b[i] = (uint32_t)g * (uint32_t)K * 16 + (uint32_t)u * 16;
+                st.voff_b[i] = (uint32_t)g * (uint32_t)Kb * 16 + (uint32_t)u * 16;
             }
         } else {
             const char* pb = (const char*)args.ptr_B + (size_t)n0 * ldb;
@@ -246,14 +262,14 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
     // of a buffer.
 #pragma unroll
     for (int p = 0; p < C::NS - 1; p++)
-        issue_stage<C>(st, smem, p, p, kb + p * 128, wave);
+        issue_stage<C>(st, smem, p, p, kbb + p * 128, wave);
     int buf = 0;
     for (int s = 0; s < nsteps; s++) {
         wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
         barrier_lds();
         int nbuf = buf + C::NS - 1;
         nbuf = nbuf >= C::NS ? nbuf - C::NS : nbuf;
-        issue_stage<C>(st, smem, nbuf, s + C::NS - 1, kb + (s + C::NS - 1) * 128, wave);
+        issue_stage<C>(st, smem, nbuf, s + C::NS - 1, kbb + (s + C::NS - 1) * 128, wave);
         __builtin_amdgcn_sched_barrier(0);
         compute_stage<C>(smem, buf, s, wm, wn, lane, acc);
         __builtin_amdgcn_sched_barrier(0);
@@ -319,6 +335,11 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
      &FN, 64, 8}
 // MXFP4 (the reference's f4gemm_bf16_per1x32Fp4 kernels): e2m1 operands.
+#define GA_MX4_ENTRY(BM, BN, WGM, WGN, BPS, NS, SPLIT, SUFFIX)                                 \
+    {{BM, BN, SPLIT, BPS,                                                                     \
+      "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
+      "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS, true>>, 32, 4}
 #define GA_MX4_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                \
     {{256, 256, SPLIT, BPS, "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
@@ -343,14 +364,27 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
     // not in the manifest: the 4-wave 256x256 tile (two stages)
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
-    // the MXFP4 manifest
+    // the MXFP4 manifest, the MXFP8 one's tiles and order
     GA_MX4_PP_ENTRY(1, 0, "", launch_mx4_pp_bps),
+    GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
+    GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
+    GA_MX4_ENTRY(128, 128, 2, 2, 1, 4, 0, ""),
+    GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
+    GA_MX4_ENTRY(32, 256, 1, 4, 1, 4, 0, ""),
     GA_MX4_PP_ENTRY(1, 1, "_splitK", launch_mx4_pp_bps),
+    GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
+    GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
+    GA_MX4_ENTRY(128, 128, 2, 2, 1, 4, 1, "_splitK"),
+    GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
+    GA_MX4_ENTRY(32, 256, 1, 4, 1, 4, 1, "_splitK"),
+    GA_MX4_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
     GA_MX4_PP_ENTRY(0, 0, "", launch_mx4_pp_nobps),
+    GA_MX4_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
+    GA_MX4_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
 };
 constexpr int kManifestCount = 16;
 constexpr int kMx4First = 17;
-constexpr int kMx4Count = 3;
+constexpr int kMx4Count = 16;
 
 int mx_registry_count() { return kManifestCount; }
 int mx4_registry_first() { return kMx4First; }

@@ -71,18 +71,25 @@ def check4(got, qa, sa, qb, sb, l2, label):
     return st
 
 
+FP4_MANIFEST = ["ga_mxfp4_bf16_BpreShuffle_%s" % t for t in
+                ("256x256", "256x128", "128x256", "128x128", "64x256", "32x256")] + \
+               ["ga_mxfp4_bf16_BpreShuffle_%s_splitK" % t for t in
+                ("256x256", "256x128", "128x256", "128x128", "64x256", "32x256", "32x512")] + \
+               ["ga_mxfp4_bf16_noBpreShuffle_256x256", "ga_mxfp4_bf16_noBpreShuffle_256x128",
+                "ga_mxfp4_bf16_noBpreShuffle_128x128_splitK"]
+
+
 def test_manifest_fp4_rows():
+    """The MXFP4 manifest carries the MXFP8 manifest's tiles in its order."""
     rows = f4gemm.manifest_fp4()
-    assert [c.knl_name for c in rows] == ["ga_mxfp4_bf16_BpreShuffle_256x256",
-                                          "ga_mxfp4_bf16_BpreShuffle_256x256_splitK",
-                                          "ga_mxfp4_bf16_noBpreShuffle_256x256"]
+    assert [c.knl_name for c in rows] == FP4_MANIFEST
+    assert [c.knl_name.replace("mxfp4", "mxfp8") for c in rows] == \
+        [c.knl_name for c in f4gemm.manifest()]
     assert f4gemm.manifest_fp4_csv().splitlines()[0] == \
         "tile_M,tile_N,splitK,bpreshuffle,knl_name,co_name"
 
 
-@pytest.mark.parametrize("name", ["ga_mxfp4_bf16_BpreShuffle_256x256",
-                                  "ga_mxfp4_bf16_BpreShuffle_256x256_splitK",
-                                  "ga_mxfp4_bf16_noBpreShuffle_256x256"])
+@pytest.mark.parametrize("name", FP4_MANIFEST)
 def test_every_fp4_kernel(dev, name):
     M, N, K = 300, 2048, 1024
     qa, sa, qb, sb = mx4_operands(M, N, K, seed=3)
@@ -97,17 +104,21 @@ def test_fp4_edge_shapes(dev, shape):
     """Partial M and N tiles, one or an odd number of 256-K steps, one row."""
     M, N, K = shape
     qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + N + K)
-    for name in ("ga_mxfp4_bf16_BpreShuffle_256x256", "ga_mxfp4_bf16_noBpreShuffle_256x256"):
+    for name in ("ga_mxfp4_bf16_BpreShuffle_256x256", "ga_mxfp4_bf16_noBpreShuffle_256x256",
+                 "ga_mxfp4_bf16_BpreShuffle_128x128", "ga_mxfp4_bf16_noBpreShuffle_256x128"):
         got = run_mx4(dev, qa, sa, qb, sb, cfg4(name))
         check4(got, qa, sa, qb, sb, 0, "%s %s" % (shape, name))
 
 
 @pytest.mark.parametrize("l2", [1, 2, 3])
-def test_fp4_splitk(dev, l2):
+@pytest.mark.parametrize("name", ["ga_mxfp4_bf16_BpreShuffle_256x256_splitK",
+                                  "ga_mxfp4_bf16_BpreShuffle_128x128_splitK",
+                                  "ga_mxfp4_bf16_noBpreShuffle_128x128_splitK"])
+def test_fp4_splitk(dev, l2, name):
     M, N, K = 96, 1024, 4096
     qa, sa, qb, sb = mx4_operands(M, N, K, seed=7 + l2)
-    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_BpreShuffle_256x256_splitK"), l2)
-    check4(got, qa, sa, qb, sb, l2, "splitK L=%d" % l2)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4(name), l2)
+    check4(got, qa, sa, qb, sb, l2, "%s L=%d" % (name, l2))
 
 
 @pytest.mark.parametrize("M", [1, 16, 17, 33, 64])
