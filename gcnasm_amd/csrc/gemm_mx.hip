@@ -64,6 +64,9 @@ struct MxCfg {
     static constexpr int S_BYTES = 4 * S_LOADS * 256;
     static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
     static constexpr int LDS = NS * STAGE;
+    // Two workgroups per CU when two fit in LDS: with more tiles than CUs the
+    // second one's copies and MFMAs fill the first one's waits.
+    static constexpr int WPE = 2 * LDS <= 160 * 1024 ? 2 : 1;
     static constexpr int A_LOADS = A_BYTES / (NT * 16);
     static constexpr int B_LOADS = B_BYTES / (NT * 16);
     static constexpr int TILE_LOADS = A_LOADS + B_LOADS + S_LOADS; // vmem ops per stage
@@ -172,7 +175,7 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
 }
 
 template <class C>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(C::WPE, C::WPE)))
 void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
 {
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
@@ -349,38 +352,38 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
-    GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 0, ""),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 2, 0, ""),
     GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 0, ""),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 2, 0, ""),
     GA_MX_PP_ENTRY(1, 1, "_splitK", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
-    GA_MX_ENTRY(128, 128, 2, 2, 1, 4, 1, "_splitK"),
+    GA_MX_ENTRY(128, 128, 2, 2, 1, 2, 1, "_splitK"),
     GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 4, 1, "_splitK"),
+    GA_MX_ENTRY(32, 256, 1, 4, 1, 2, 1, "_splitK"),
     GA_MX_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
     GA_MX_PP_ENTRY(0, 0, "", launch_mx_pp_nobps),
     GA_MX_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
-    GA_MX_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
+    GA_MX_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
     // not in the manifest: the 4-wave 256x256 tile (two stages)
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
     // the MXFP4 manifest, the MXFP8 one's tiles and order
     GA_MX4_PP_ENTRY(1, 0, "", launch_mx4_pp_bps),
     GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
     GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
-    GA_MX4_ENTRY(128, 128, 2, 2, 1, 4, 0, ""),
+    GA_MX4_ENTRY(128, 128, 2, 2, 1, 2, 0, ""),
     GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
-    GA_MX4_ENTRY(32, 256, 1, 4, 1, 4, 0, ""),
+    GA_MX4_ENTRY(32, 256, 1, 4, 1, 2, 0, ""),
     GA_MX4_PP_ENTRY(1, 1, "_splitK", launch_mx4_pp_bps),
     GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
-    GA_MX4_ENTRY(128, 128, 2, 2, 1, 4, 1, "_splitK"),
+    GA_MX4_ENTRY(128, 128, 2, 2, 1, 2, 1, "_splitK"),
     GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
-    GA_MX4_ENTRY(32, 256, 1, 4, 1, 4, 1, "_splitK"),
+    GA_MX4_ENTRY(32, 256, 1, 4, 1, 2, 1, "_splitK"),
     GA_MX4_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
     GA_MX4_PP_ENTRY(0, 0, "", launch_mx4_pp_nobps),
     GA_MX4_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
-    GA_MX4_ENTRY(128, 128, 2, 2, 0, 4, 1, "_splitK"),
+    GA_MX4_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
 };
 constexpr int kManifestCount = 16;
 constexpr int kMx4First = 17;
