@@ -161,3 +161,23 @@ def test_splitk_reduce(dev):
     O.or_splitk_reduce(oracle.p(ws), oracle.p(want), split, M, N, batch, pM, pN, None, 0)
     np.testing.assert_array_equal(outb.view(torch.int16).cpu().numpy().view(np.uint16),
                                   oracle.to_bf16_bits(want))
+
+
+@pytest.mark.parametrize("dims", [(5, 3, 5000, 2, 8, 5008), (2, 70, 37, 1, 72, 40),
+                                  (9, 1, 2048, 3, 1, 2048), (1, 300, 8, 1, 300, 8)])
+def test_splitk_reduce_shapes(dev, dims):
+    """Rows wider than one workgroup (several along N), rows packed several to
+    a workgroup, N tails that are not a multiple of 8, one slice."""
+    split, M, N, batch, pM, pN = dims
+    rng = np.random.default_rng(split * 1000 + N)
+    ws = rng.standard_normal((split, batch, pM, pN)).astype(np.float32)
+    bias = rng.standard_normal((batch, N)).astype(np.float32)
+    want = np.empty((batch, M, N), dtype=np.float32)
+    O = oracle.load()
+    O.or_splitk_reduce(oracle.p(ws), oracle.p(want), split, M, N, batch, pM, pN,
+                       oracle.p(bias), N)
+    out = torch.full((batch, M, N), float("nan"), dtype=torch.float32, device=dev)
+    ops.splitk_reduce(torch.from_numpy(ws).to(dev), out, split, M, N, batch, pM, pN,
+                      bias=torch.from_numpy(bias).to(dev))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
