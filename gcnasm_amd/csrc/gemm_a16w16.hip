@@ -22,6 +22,9 @@
 //    (K [32, 64)).
 //  * Operands swapped (B rows on the MFMA's A side), so a lane ends with 4
 //    consecutive N outputs of one C row -> 16-byte fp32 stores.
+//  * The fragments of K step s+1 are read from LDS while the MFMAs of step s
+//    run (two register sets): with one wave per SIMD nothing else would hide
+//    the LDS read latency of every step.
 //  * Slices follow the reference's partition (pipeline .cuh:234-247): K in
 //    128-element iterations, ceil(iters / split_k) per slice, the last slice
 //    takes what is left; a slice left empty writes zeros. Chunks at or past
@@ -57,7 +60,7 @@ struct A16Cfg {
     static constexpr int TILE_LOADS = A_LOADS + B_LOADS;
     static_assert(BM % 32 == 0 && BN % 32 == 0, "tile multiple of 32 rows");
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(NS >= 2 && TILE_LOADS * (NS - 2) < 64, "vmcnt range");
+    static_assert(NS >= 3 && TILE_LOADS * (NS - 2) < 64, "vmcnt range");
 };
 
 struct A16Args {
@@ -101,36 +104,46 @@ __device__ __forceinline__ void a16_issue(const A16State<C>& st, char* smem, int
                    ok ? st.voff_b[i] + kbytes : 0xFFFFFFF0u, 0);
 }
 
+// Operand fragments of one K step: [K half][tile].
 template <class C>
-__device__ __forceinline__ void a16_compute(const char* smem, int buf, int wm, int wn, int lane,
-                                            v4f (&acc)[C::TM][C::TN])
+struct A16Frag {
+    v4i a[2][C::TM], b[2][C::TN];
+};
+
+template <class C>
+__device__ __forceinline__ void a16_read(const char* smem, int buf, int wm, int wn, int lane,
+                                         A16Frag<C>& f)
 {
     const char* la = smem + buf * C::STAGE;
     const char* lb = la + C::A_BYTES;
     uint32_t o0, o1;
     pp::operand_lane(lane, o0, o1);
-    v4i a[2][C::TM], b[2][C::TN];
 #pragma unroll
     for (int t = 0; t < C::TN; t++) {
         const char* g = lb + (wn * C::TN + t) * 2048;
-        b[0][t] = *(const v4i*)(g + o0);
-        b[1][t] = *(const v4i*)(g + o1);
+        f.b[0][t] = *(const v4i*)(g + o0);
+        f.b[1][t] = *(const v4i*)(g + o1);
     }
 #pragma unroll
     for (int i = 0; i < C::TM; i++) {
         const char* g = la + (wm * C::TM + i) * 2048;
-        a[0][i] = *(const v4i*)(g + o0);
-        a[1][i] = *(const v4i*)(g + o1);
+        f.a[0][i] = *(const v4i*)(g + o0);
+        f.a[1][i] = *(const v4i*)(g + o1);
     }
-    // K [0, 32) over every accumulator, then K [32, 64): no back-to-back
-    // dependent MFMAs
+}
+
+// K [0, 32) over every accumulator, then K [32, 64): no back-to-back
+// dependent MFMAs
+template <class C>
+__device__ __forceinline__ void a16_mma(const A16Frag<C>& f, v4f (&acc)[C::TM][C::TN])
+{
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int t = 0; t < C::TN; t++)
-                acc[i][t] = mfma_bf16_16x16x32(b[h][t], a[h][i], acc[i][t]);
+                acc[i][t] = mfma_bf16_16x16x32(f.b[h][t], f.a[h][i], acc[i][t]);
 }
 
 // Writes acc (+ bias) as bf16 C; lane holds C[m][n .. n+3] of each 16x16 tile.
@@ -249,25 +262,40 @@ void a16w16_splitk_kernel(A16Args p)
         for (int j = 0; j < C::TN; j++)
             acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    // Pipeline: NS-1 stages in flight; step s waits for its stage (counted
-    // vmcnt: the loop's only memory reads are direct-to-LDS copies), then
-    // refills the buffer step s-1 used (free after the barrier) with stage
-    // s+NS-1 and computes from stage s.
+    // Pipeline: NS-1 stages in flight, and the operand fragments of step s+1
+    // read from LDS while the MFMAs of step s run. Step s waits for stage s+1
+    // (counted vmcnt: the loop's only memory reads are direct-to-LDS copies;
+    // the barrier also ends every wave's fragment reads of stage s), refills
+    // the buffer step s-1 used with stage s+NS-1, reads the fragments of
+    // stage s+1, then multiplies the fragments of stage s read one step
+    // earlier. Two fragment sets alternate (the loop is unrolled by two).
 #pragma unroll
     for (int q = 0; q < C::NS - 1; q++)
         a16_issue<C>(st, smem, q, q, kb, ke, wave);
-    int buf = 0;
-    for (int s = 0; s < nsteps; s++) {
-        wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
+    A16Frag<C> f0, f1;
+    wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
+    barrier_lds();
+    a16_read<C>(smem, 0, wm, wn, lane, f0);
+    int buf = 0; // LDS buffer of stage s
+    auto step = [&](int s, const A16Frag<C>& cur, A16Frag<C>& nxt) {
+        wait_vmcnt<C::TILE_LOADS * (C::NS - 3)>();
         barrier_lds();
-        int nbuf = buf + C::NS - 1;
-        nbuf = nbuf >= C::NS ? nbuf - C::NS : nbuf;
-        a16_issue<C>(st, smem, nbuf, s + C::NS - 1, kb, ke, wave);
+        const int prev = buf == 0 ? C::NS - 1 : buf - 1;
+        const int next = buf + 1 == C::NS ? 0 : buf + 1;
+        a16_issue<C>(st, smem, prev, s + C::NS - 1, kb, ke, wave);
         __builtin_amdgcn_sched_barrier(0);
-        a16_compute<C>(smem, buf, wm, wn, lane, acc);
+        a16_read<C>(smem, next, wm, wn, lane, nxt);
+        a16_mma<C>(cur, acc);
         __builtin_amdgcn_sched_barrier(0);
-        buf = buf + 1 == C::NS ? 0 : buf + 1;
+        buf = next;
+    };
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        step(s, f0, f1);
+        step(s + 1, f1, f0);
     }
+    if (s < nsteps)
+        step(s, f0, f1);
     // drain the prefetches past the slice before the workgroup's LDS is freed
     wait_vmcnt<0>();
 
@@ -320,10 +348,10 @@ static ga_status launch_a16(const ga_flatmm_splitk_kargs& ka, int kslice, hipStr
 // sized problems and the skinny 1024x512x7168): the largest tile whose grid
 // still gives every CU a workgroup wins; 128-row tiles are not used for M up
 // to 64 (they would compute mostly padding).
-typedef A16Cfg<128, 256, 2> A16Huge;
-typedef A16Cfg<128, 128, 3> A16Big;
+typedef A16Cfg<128, 256, 3> A16Huge;
+typedef A16Cfg<128, 128, 4> A16Big;
 typedef A16Cfg<64, 128, 4> A16Mid;
-typedef A16Cfg<64, 64, 4> A16Small;
+typedef A16Cfg<64, 64, 6> A16Small;
 
 template <int EPI>
 static ga_status dispatch_a16(const ga_flatmm_splitk_kargs& ka, hipStream_t stream)
