@@ -26,6 +26,10 @@
 //  * The shuffled scale layout puts, for each 32 rows x 256 K, the scales of
 //    lane l (row l%16, K-block l/16) in dword l; the byte inside the dword
 //    (row half, 128-K half) is picked with the MFMA's op_sel.
+//  * Preshuffled-B entries with 32 or 64 rows (32x256, 64x256, 32x512) run a
+//    B-streaming tile instead: waves side by side along N, B loaded straight
+//    into the MFMA operand registers 4 steps deep, only A and the scales in
+//    LDS (mx_bstream_kernel).
 //  * Split-K (gdz > 1): each K slice writes fp32 partials to a workspace;
 //    the reduce kernel sums the slices in order and applies the epilogue.
 //  * Tile order: workgroup ids are dispatched round-robin over the 8 XCDs;
@@ -174,6 +178,49 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
     });
 }
 
+// Epilogue of a wave's TM x TN 16x16 tiles starting at (mb, nb): lane holds
+// C[m][n .. n+3] of each tile. Split-K slices write fp32 partials; otherwise
+// D = bf16(alpha * acc (+ beta * C)). The library is built with
+// -ffp-contract=off: alpha*v and + beta*c round separately.
+template <int TM, int TN>
+__device__ __forceinline__ void mx_store(const ga_f4gemm_kargs& args, float* ws, int z, int gdz,
+                                         int mb, int nb, int lane, const v4f (&acc)[TM][TN])
+{
+    const int M = (int)args.M, N = (int)args.N;
+    const int ldd = (int)args.stride_C0;
+    const float alpha = args.alpha, beta = args.beta;
+    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int m = mb + i * 16 + (lane & 15);
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            const int n = nb + t * 16 + (lane >> 4) * 4;
+            if (m >= M || n >= N)
+                continue;
+            v4f v = acc[i][t];
+            if (gdz > 1) {
+                *(v4f*)(ws + ((size_t)z * M + m) * N + n) = v;
+            } else {
+                uint16_t o[4];
+                const uint16_t* cin = use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n
+                                            : nullptr;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float r = alpha * v[j];
+                    if (use_c)
+                        r = r + beta * bf16_to_f32(cin[j]);
+                    o[j] = f32_to_bf16(r);
+                }
+                uint2 pk;
+                pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+                pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+                *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+            }
+        }
+    }
+}
+
 template <class C>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(C::WPE, C::WPE)))
 void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
@@ -278,41 +325,10 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         __builtin_amdgcn_sched_barrier(0);
         buf = buf + 1 == C::NS ? 0 : buf + 1;
     }
+    // the copies of steps past the slice land before the workgroup's LDS is freed
+    wait_vmcnt<0>();
 
-    // Epilogue: lane holds C[m][n .. n+3] of each 16x16 tile. The library is
-    // built with -ffp-contract=off: alpha*v and + beta*c round separately.
-    const int ldd = (int)args.stride_C0;
-    const float alpha = args.alpha, beta = args.beta;
-    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
-#pragma unroll
-    for (int i = 0; i < C::TM; i++) {
-        const int m = m0 + wm * C::WTM + i * 16 + (lane & 15);
-#pragma unroll
-        for (int t = 0; t < C::TN; t++) {
-            const int n = n0 + wn * C::WTN + t * 16 + (lane >> 4) * 4;
-            if (m >= M || n >= N)
-                continue;
-            v4f v = acc[i][t];
-            if (gdz > 1) {
-                *(v4f*)(ws + ((size_t)z * M + m) * N + n) = v;
-            } else {
-                uint16_t o[4];
-                const uint16_t* cin = use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n
-                                            : nullptr;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float r = alpha * v[j];
-                    if (use_c)
-                        r = r + beta * bf16_to_f32(cin[j]);
-                    o[j] = f32_to_bf16(r);
-                }
-                uint2 pk;
-                pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-                pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-                *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
-            }
-        }
-    }
+    mx_store<C::TM, C::TN>(args, ws, z, gdz, m0 + wm * C::WTM, n0 + wn * C::WTN, lane, acc);
 }
 
 template <class C>
@@ -322,11 +338,236 @@ static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, 
     hipLaunchKernelGGL(mx_gemm_kernel<C>, dim3(gdx, gdy, gdz), dim3(256), 0, stream, args, ws);
 }
 
+// B-streaming tile for preshuffled B and few rows (BM = 32 or 64): the four
+// waves sit side by side along N, so no wave shares a B fragment with
+// another, and B goes from memory straight into the MFMA operand registers
+// (a ring of NS K steps in flight per wave: the preshuffled 2 KB of a 16-row
+// group and 128-K step is the operand of 64 lanes as it lies). Only A (BM
+// rows, read by all four waves) and the scales pass through LDS, so the
+// pipeline depth is bounded by registers, not by LDS: with LDS-staged B the
+// 32-row tiles kept one or two steps in flight and waited a memory latency
+// per step.
+template <int BM_, int BN_, int NS_, bool FP4_>
+struct MbCfg {
+    static constexpr int BM = BM_, BN = BN_, NS = NS_;
+    static constexpr bool FP4 = FP4_;
+    static constexpr int EPB = FP4 ? 2 : 1;
+    static constexpr int NT = 256;
+    static constexpr int WTN = BN / 4;
+    static constexpr int TM = BM / 16, TN = WTN / 16;
+    static constexpr int SM = TM / 2, SN = TN / 2;
+    static constexpr int A_BYTES = BM * 128;
+    static constexpr int SBLK = BM / 32 + BN / 32;
+    static constexpr int S_LOADS = (SBLK + 3) / 4;
+    static constexpr int S_BYTES = 4 * S_LOADS * 256;
+    static constexpr int STAGE = A_BYTES + S_BYTES;
+    static constexpr int LDS = NS * STAGE;
+    static constexpr int A_LOADS = A_BYTES / (NT * 16);
+    static constexpr int B_LOADS = 2 * TN; // per wave per step, into registers
+    static constexpr int TILE_LOADS = A_LOADS + B_LOADS + S_LOADS;
+    static_assert(BM % 32 == 0 && WTN % 32 == 0, "32-row scale blocks");
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(NS >= 2 && TILE_LOADS * (NS - 2) < 64, "vmcnt range");
+};
+
+template <class C>
+struct MbState {
+    __amdgpu_buffer_rsrc_t ra, rb, rsa, rsb;
+    uint32_t voff_a[C::A_LOADS];
+    uint32_t vb;      // this lane's byte in the wave's first 16-row B group
+    uint32_t gstride; // bytes between 16-row B groups (16 * K bytes)
+    uint32_t soff[C::S_LOADS];
+    bool sfrom_b[C::S_LOADS];
+};
+
+// Step `step` (byte offset kk inside a row): A and scales into LDS stage
+// `buf`, this wave's B fragments into bq.
+template <class C>
+__device__ __forceinline__ void mb_issue(const MbState<C>& st, char* smem, int buf, int step,
+                                         int kk, int wave, v8i (&bq)[C::TN])
+{
+    char* sa = smem + buf * C::STAGE;
+    char* ss = sa + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < C::A_LOADS; i++)
+        lds_load16(st.ra, (lds_void*)(sa + (i * 256 + wave * 64) * 16), st.voff_a[i] + kk, 0);
+    const uint32_t q = (uint32_t)(C::FP4 ? step : (step >> 1)) * 256;
+#pragma unroll
+    for (int i = 0; i < C::S_LOADS; i++) {
+        lds_void* dst = (lds_void*)(ss + (wave * C::S_LOADS + i) * 256);
+        if (st.sfrom_b[i])
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(st.rsb, dst, 4, st.soff[i] + q, 0, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(st.rsa, dst, 4, st.soff[i] + q, 0, 0, 0);
+    }
+    const uint32_t kq = (uint32_t)(kk / 128) * 2048;
+#pragma unroll
+    for (int t = 0; t < C::TN; t++) {
+        const uint32_t o = st.vb + __builtin_amdgcn_readfirstlane((uint32_t)t * st.gstride + kq);
+        v4i x0 = buf_load16(st.rb, o, 0);
+        v4i x1 = buf_load16(st.rb, o + 1024, 0);
+        bq[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void mb_compute(const char* smem, int buf, int step, int wn, int lane,
+                                           const v8i (&bq)[C::TN], v4f (&acc)[C::TM][C::TN])
+{
+    const char* la = smem + buf * C::STAGE;
+    const char* ls = la + C::A_BYTES;
+    uint32_t o0, o1;
+    pp::operand_lane(lane, o0, o1);
+    const uint32_t sh = C::FP4 ? 0u : (uint32_t)(step & 1) * 16;
+    uint32_t sa[C::SM], sb[C::SN];
+#pragma unroll
+    for (int t = 0; t < C::SM; t++)
+        sa[t] = *(const uint32_t*)(ls + t * 256 + lane * 4) >> sh;
+#pragma unroll
+    for (int t = 0; t < C::SN; t++)
+        sb[t] = *(const uint32_t*)(ls + (C::BM / 32 + wn * C::SN + t) * 256 + lane * 4) >> sh;
+    static_for<C::TM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
+        const char* g = la + i * 2048;
+        v4i x0 = *(const v4i*)(g + o0);
+        v4i x1 = *(const v4i*)(g + o1);
+        v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        static_for<C::TN>([&](auto T) {
+            constexpr int t = decltype(T)::value;
+            if constexpr (C::FP4) {
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(bq[t], af, acc[i][t],
+                                                             (int)sb[t >> 1], (int)sa[i >> 1]);
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(hi16(bq[t]), hi16(af), acc[i][t],
+                                                             (int)(sb[t >> 1] >> 16),
+                                                             (int)(sa[i >> 1] >> 16));
+            } else {
+                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(bq[t], af, acc[i][t], (int)sb[t >> 1],
+                                                        (int)sa[i >> 1]);
+            }
+        });
+    });
+}
+
+template <class C>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void mx_bstream_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
+{
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+    int tile_m, tile_n;
+    map_tile(blockIdx.x, blockIdx.y, gridDim.x, gridDim.y, kGroupM, tile_m, tile_n);
+    const int m0 = tile_m * C::BM, n0 = tile_n * C::BN;
+    const int z = blockIdx.z, gdz = gridDim.z;
+    int kpt = K;
+    if (gdz > 1)
+        kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
+    const int kb = z * kpt;
+    const int ke = min(K, kb + kpt);
+    const int nsteps = (ke - kb) / (128 * C::EPB);
+    const int kbb = kb / C::EPB, Kb = K / C::EPB; // bytes
+    const uint32_t lda = args.stride_A0 / C::EPB;
+    const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
+
+    MbState<C> st;
+    {
+        const char* pa = (const char*)args.ptr_A + (size_t)m0 * lda;
+        long long abytes = (long long)(M - m0) * lda;
+        st.ra = make_rsrc(pa, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+        int row0, chunk;
+        pp::copy_lane(wave, lane, row0, chunk);
+#pragma unroll
+        for (int i = 0; i < C::A_LOADS; i++)
+            st.voff_a[i] = (uint32_t)(i * 32 + row0) * lda + chunk * 16;
+        // preshuffled B: 16-row group g of the tile holds its K steps as
+        // consecutive 2 KB blocks; rows past N read as zero
+        const char* pb = (const char*)args.ptr_B + (size_t)(n0 / 16) * Kb * 16;
+        long long bbytes = (long long)(N - n0) * Kb;
+        st.rb = make_rsrc(pb, (uint32_t)(bbytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : bbytes));
+        st.gstride = (uint32_t)Kb * 16;
+        st.vb = (uint32_t)(wave * C::TN) * st.gstride + (uint32_t)lane * 16;
+        const int sma = (M + 31) / 32 * 32, smb = (N + 31) / 32 * 32;
+        st.rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)sma * sna);
+        st.rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)smb * snb);
+        const int q0 = kb / 256;
+#pragma unroll
+        for (int i = 0; i < C::S_LOADS; i++) {
+            int j = wave * C::S_LOADS + i;
+            j = j < C::SBLK ? j : 0; // padding slots repeat block 0
+            const bool isb = j >= C::BM / 32;
+            const int r = isb ? n0 + (j - C::BM / 32) * 32 : m0 + j * 32;
+            const uint32_t sn = isb ? snb : sna;
+            st.sfrom_b[i] = isb;
+            st.soff[i] = ((uint32_t)(r / 32) * (sn / 8) + q0) * 256 + lane * 4;
+        }
+    }
+
+    v4f acc[C::TM][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int t = 0; t < C::TN; t++)
+            acc[i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    // Pipeline: steps 0 .. NS-2 in flight before the loop. Step s (ring slot
+    // s % NS, a compile-time index: the loop is unrolled NS times) waits for
+    // its A and scale copies (counted vmcnt; the compiler adds the waits for
+    // the B registers itself), then issues step s+NS-1 into the slot step
+    // s-1 used and multiplies.
+    v8i bq[C::NS][C::TN];
+    static_for<C::NS - 1>([&](auto P) {
+        constexpr int p = decltype(P)::value;
+        mb_issue<C>(st, smem, p, p, kbb + p * 128, wave, bq[p]);
+    });
+    for (int s0 = 0; s0 < nsteps; s0 += C::NS) {
+        static_for<C::NS>([&](auto P) {
+            constexpr int p = decltype(P)::value;
+            constexpr int np = (p + C::NS - 1) % C::NS;
+            const int s = s0 + p;
+            if (s < nsteps) {
+                wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
+                barrier_lds();
+                mb_issue<C>(st, smem, np, s + C::NS - 1, kbb + (s + C::NS - 1) * 128, wave,
+                            bq[np]);
+                __builtin_amdgcn_sched_barrier(0);
+                mb_compute<C>(smem, p, s, wave, lane, bq[p], acc);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+    }
+    // the loads of steps past the slice land before the workgroup ends
+    wait_vmcnt<0>();
+    mx_store<C::TM, C::TN>(args, ws, z, gdz, m0, n0 + wave * C::WTN, lane, acc);
+}
+
+// Entry tiles BM x BN run as workgroups of C::BN columns (BN a multiple of
+// C::BN): the entry's grid fixes the tile a caller sees; a 32x512 workgroup
+// would leave half of the CUs idle at M <= 128.
+template <class C>
+static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
+                       hipStream_t stream)
+{
+    (void)gdx;
+    const int gx = ((int)args.N + C::BN - 1) / C::BN;
+    hipLaunchKernelGGL(mx_bstream_kernel<C>, dim3(gx, gdy, gdz), dim3(256), 0, stream, args, ws);
+}
+
 #define GA_MX_ENTRY(BM, BN, WGM, WGN, BPS, NS, SPLIT, SUFFIX)                                  \
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
      &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 32, 8}
+// Preshuffled-B entries with 32 or 64 rows run the B-streaming tile (IBN
+// columns per workgroup, 4 steps in flight).
+#define GA_MXB_ENTRY(BM, BN, IBN, SPLIT, SUFFIX)                                               \
+    {{BM, BN, SPLIT, 1, "ga_mxfp8_bf16_BpreShuffle_" #BM "x" #BN SUFFIX,                      \
+      "ga_mxfp8_bf16_BpreShuffle_" #BM "x" #BN SUFFIX ".co"},                                 \
+     &launch_mxb<MbCfg<BM, IBN, 4, false>>, 32, 8}
+#define GA_MX4B_ENTRY(BM, BN, IBN, SPLIT, SUFFIX)                                              \
+    {{BM, BN, SPLIT, 1, "ga_mxfp4_bf16_BpreShuffle_" #BM "x" #BN SUFFIX,                      \
+      "ga_mxfp4_bf16_BpreShuffle_" #BM "x" #BN SUFFIX ".co"},                                 \
+     &launch_mxb<MbCfg<BM, IBN, 4, true>>, 32, 4}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
@@ -353,15 +594,15 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
     GA_MX_ENTRY(128, 128, 2, 2, 1, 2, 0, ""),
-    GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 2, 0, ""),
+    GA_MXB_ENTRY(64, 256, 256, 0, ""),
+    GA_MXB_ENTRY(32, 256, 256, 0, ""),
     GA_MX_PP_ENTRY(1, 1, "_splitK", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX_ENTRY(128, 128, 2, 2, 1, 2, 1, "_splitK"),
-    GA_MX_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
-    GA_MX_ENTRY(32, 256, 1, 4, 1, 2, 1, "_splitK"),
-    GA_MX_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
+    GA_MXB_ENTRY(64, 256, 256, 1, "_splitK"),
+    GA_MXB_ENTRY(32, 256, 256, 1, "_splitK"),
+    GA_MXB_ENTRY(32, 512, 256, 1, "_splitK"),
     GA_MX_PP_ENTRY(0, 0, "", launch_mx_pp_nobps),
     GA_MX_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
     GA_MX_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
@@ -372,15 +613,15 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
     GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 0, ""),
     GA_MX4_ENTRY(128, 128, 2, 2, 1, 2, 0, ""),
-    GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 0, ""),
-    GA_MX4_ENTRY(32, 256, 1, 4, 1, 2, 0, ""),
+    GA_MX4B_ENTRY(64, 256, 256, 0, ""),
+    GA_MX4B_ENTRY(32, 256, 256, 0, ""),
     GA_MX4_PP_ENTRY(1, 1, "_splitK", launch_mx4_pp_bps),
     GA_MX4_ENTRY(256, 128, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX4_ENTRY(128, 256, 2, 2, 1, 3, 1, "_splitK"),
     GA_MX4_ENTRY(128, 128, 2, 2, 1, 2, 1, "_splitK"),
-    GA_MX4_ENTRY(64, 256, 1, 4, 1, 3, 1, "_splitK"),
-    GA_MX4_ENTRY(32, 256, 1, 4, 1, 2, 1, "_splitK"),
-    GA_MX4_ENTRY(32, 512, 1, 4, 1, 2, 1, "_splitK"),
+    GA_MX4B_ENTRY(64, 256, 256, 1, "_splitK"),
+    GA_MX4B_ENTRY(32, 256, 256, 1, "_splitK"),
+    GA_MX4B_ENTRY(32, 512, 256, 1, "_splitK"),
     GA_MX4_PP_ENTRY(0, 0, "", launch_mx4_pp_nobps),
     GA_MX4_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
     GA_MX4_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
