@@ -124,9 +124,16 @@ __device__ __forceinline__ void issue_stage(const MxState<C>& st, char* smem, in
     }
 }
 
+// Operand fragments and scale dwords of one K step.
 template <class C>
-__device__ __forceinline__ void compute_stage(const char* smem, int buf, int step, int wm, int wn,
-                                              int lane, v4f (&acc)[C::TM][C::TN])
+struct MxFrag {
+    uint32_t sa[C::SM], sb[C::SN];
+    v8i af[C::TM], bf[C::TN];
+};
+
+template <class C>
+__device__ __forceinline__ void read_stage(const char* smem, int buf, int step, int wm, int wn,
+                                           int lane, MxFrag<C>& f)
 {
     const char* la = smem + buf * C::STAGE;
     const char* lb = la + C::A_BYTES;
@@ -137,42 +144,48 @@ __device__ __forceinline__ void compute_stage(const char* smem, int buf, int ste
     const uint32_t b0 = C::BPS ? (uint32_t)lo : o0, b1 = C::BPS ? (uint32_t)lo + 1024 : o1;
     // MXFP8: this step's 128-K half of each scale dword moved to bytes 0-1
     const uint32_t sh = C::FP4 ? 0u : (uint32_t)(step & 1) * 16;
-    uint32_t sa[C::SM], sb[C::SN];
 #pragma unroll
     for (int t = 0; t < C::SM; t++)
-        sa[t] = *(const uint32_t*)(ls + (wm * C::SM + t) * 256 + lane * 4) >> sh;
+        f.sa[t] = *(const uint32_t*)(ls + (wm * C::SM + t) * 256 + lane * 4) >> sh;
 #pragma unroll
     for (int t = 0; t < C::SN; t++)
-        sb[t] = *(const uint32_t*)(ls + (C::BM / 32 + wn * C::SN + t) * 256 + lane * 4) >> sh;
-    v8i bf[C::TN];
+        f.sb[t] = *(const uint32_t*)(ls + (C::BM / 32 + wn * C::SN + t) * 256 + lane * 4) >> sh;
 #pragma unroll
     for (int t = 0; t < C::TN; t++) {
         const char* g = lb + (wn * C::TN + t) * 2048;
         v4i x0 = *(const v4i*)(g + b0);
         v4i x1 = *(const v4i*)(g + b1);
-        bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        f.bf[t] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
     }
-    static_for<C::TM>([&](auto I) {
-        constexpr int i = decltype(I)::value;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
         const char* g = la + (wm * C::TM + i) * 2048;
         v4i x0 = *(const v4i*)(g + o0);
         v4i x1 = *(const v4i*)(g + o1);
-        v8i af = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        f.af[i] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void mma_stage(const MxFrag<C>& f, v4f (&acc)[C::TM][C::TN])
+{
+    static_for<C::TM>([&](auto I) {
+        constexpr int i = decltype(I)::value;
         static_for<C::TN>([&](auto T) {
             constexpr int t = decltype(T)::value;
             // op_sel picks the 16-row half inside the 32-row scale block; the
             // 128-K half is the dword's low 16 bits (MXFP8: shifted there
-            // above; MXFP4: the first of the step's two MFMAs, the second
+            // when read; MXFP4: the first of the step's two MFMAs, the second
             // takes the high 16 bits and the fragments' last 16 bytes)
             if constexpr (C::FP4) {
-                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(bf[t], af, acc[i][t],
-                                                             (int)sb[t >> 1], (int)sa[i >> 1]);
-                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(hi16(bf[t]), hi16(af), acc[i][t],
-                                                             (int)(sb[t >> 1] >> 16),
-                                                             (int)(sa[i >> 1] >> 16));
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(f.bf[t], f.af[i], acc[i][t],
+                                                             (int)f.sb[t >> 1], (int)f.sa[i >> 1]);
+                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(hi16(f.bf[t]), hi16(f.af[i]), acc[i][t],
+                                                             (int)(f.sb[t >> 1] >> 16),
+                                                             (int)(f.sa[i >> 1] >> 16));
             } else {
-                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(bf[t], af, acc[i][t], (int)sb[t >> 1],
-                                                        (int)sa[i >> 1]);
+                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(f.bf[t], f.af[i], acc[i][t],
+                                                        (int)f.sb[t >> 1], (int)f.sa[i >> 1]);
             }
         });
     });
@@ -303,27 +316,59 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
         for (int t = 0; t < C::TN; t++)
             acc[i][t] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    // Pipeline: stages 0 .. NS-2 in flight before the loop; step s waits for
-    // its stage (counted vmcnt; every load of the loop is a direct-to-LDS copy,
-    // so no other wait is generated), then issues stage s+NS-1 into the buffer
-    // step s-1 used (free after the barrier) and computes from stage s. Loads
-    // past the slice are issued unconditionally (branch-free body): they read
-    // in-bounds bytes that are never used, or range-checked zeros past the end
-    // of a buffer.
+    // Pipeline: stages 0 .. NS-2 in flight before the loop. Loads past the
+    // slice are issued unconditionally (branch-free body): they read in-bounds
+    // bytes that are never used, or range-checked zeros past the end of a
+    // buffer. Every load of the loop is a direct-to-LDS copy, so the counted
+    // vmcnt waits are the only ones.
 #pragma unroll
     for (int p = 0; p < C::NS - 1; p++)
         issue_stage<C>(st, smem, p, p, kbb + p * 128, wave);
-    int buf = 0;
-    for (int s = 0; s < nsteps; s++) {
+    if constexpr (C::NS == 2) {
+        // Two stages (the tiles that run two workgroups per CU): step s waits
+        // for its stage, issues stage s+1 into the buffer step s-1 used (free
+        // after the barrier) and computes from stage s.
+        for (int s = 0; s < nsteps; s++) {
+            wait_vmcnt<0>();
+            barrier_lds();
+            issue_stage<C>(st, smem, (s + 1) & 1, s + 1, kbb + (s + 1) * 128, wave);
+            __builtin_amdgcn_sched_barrier(0);
+            MxFrag<C> f;
+            read_stage<C>(smem, s & 1, s, wm, wn, lane, f);
+            mma_stage<C>(f, acc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        // Three or more stages (one workgroup per CU, one wave per SIMD): the
+        // fragments of step s+1 are read while the MFMAs of step s run. Step s
+        // waits for stage s+1 (the barrier also ends every wave's reads of
+        // stage s), refills the buffer of step s-1 with stage s+NS-1, reads
+        // stage s+1, multiplies the fragments of stage s. Two fragment sets
+        // alternate (the loop is unrolled by two).
+        MxFrag<C> f0, f1;
         wait_vmcnt<C::TILE_LOADS * (C::NS - 2)>();
         barrier_lds();
-        int nbuf = buf + C::NS - 1;
-        nbuf = nbuf >= C::NS ? nbuf - C::NS : nbuf;
-        issue_stage<C>(st, smem, nbuf, s + C::NS - 1, kbb + (s + C::NS - 1) * 128, wave);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_stage<C>(smem, buf, s, wm, wn, lane, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        buf = buf + 1 == C::NS ? 0 : buf + 1;
+        read_stage<C>(smem, 0, 0, wm, wn, lane, f0);
+        int buf = 0; // LDS buffer of stage s
+        auto step = [&](int s, const MxFrag<C>& cur, MxFrag<C>& nxt) {
+            wait_vmcnt<C::TILE_LOADS * (C::NS - 3)>();
+            barrier_lds();
+            const int prev = buf == 0 ? C::NS - 1 : buf - 1;
+            const int next = buf + 1 == C::NS ? 0 : buf + 1;
+            issue_stage<C>(st, smem, prev, s + C::NS - 1, kbb + (s + C::NS - 1) * 128, wave);
+            __builtin_amdgcn_sched_barrier(0);
+            read_stage<C>(smem, next, s + 1, wm, wn, lane, nxt);
+            mma_stage<C>(cur, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            buf = next;
+        };
+        int s = 0;
+        for (; s + 1 < nsteps; s += 2) {
+            step(s, f0, f1);
+            step(s + 1, f1, f0);
+        }
+        if (s < nsteps)
+            step(s, f0, f1);
     }
     // the copies of steps past the slice land before the workgroup's LDS is freed
     wait_vmcnt<0>();
