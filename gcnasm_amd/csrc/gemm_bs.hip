@@ -13,13 +13,15 @@
 // through the buffer range check; a partial last N group of 128 is fine).
 // C is fp32 (the reference's output type) or bf16.
 //
-// 33-64 rows with enough columns (this file): 4 waves, 64x256 tile, K step 128, A and B
+// 33-64 rows with enough columns, or more rows with few 256x256 tiles (this
+// file): 4 waves, 64x256 or 128x128 tile, K step 128, A and B
 // staged with buffer_load ... lds (8 whole 128-byte rows per instruction)
 // into swizzled LDS rows (chunk c of row r at slot c ^ ((r >> 1) & 7)),
 // v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales (127) and the
 // operands swapped so a lane owns 4 consecutive N of one C row. More rows go
-// to the 256x256 eight-wave kernel of gemm_bs_pp.hip, fewer rows (or too few
-// 256-column tiles) to the B-streaming kernel of gemm_bs_decode.hip.
+// to the 256x256 eight-wave kernel of gemm_bs_pp.hip when its grid covers a
+// third of the CUs, fewer rows (or too few 256-column tiles) to the
+// B-streaming kernel of gemm_bs_decode.hip.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
 #include "ga_pp.hpp"
@@ -276,8 +278,20 @@ static ga_status launch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
 template <int MODE, int OUT>
 static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
 {
-    // More than 64 rows: the 256x256 eight-wave kernel (gemm_bs_pp.hip).
+    int num_cu = 0;
+    ga_status st = device_cu_count(&num_cu);
+    if (st != GA_OK)
+        return st;
+    // More than 64 rows: the 256x256 eight-wave kernel (gemm_bs_pp.hip), or
+    // this file's 128x128 tile when 256x256 tiles would cover less than a
+    // third of the CUs (measured on MI355X, fp32 C: 512x7168x2048 35.4 ->
+    // 23.5 us, 1024x4096x4096 54.9 -> 39.8 us; with 112 or more 256x256
+    // tiles the eight-wave kernel is faster).
     if (ka.m > 64) {
+        const long long t256 =
+            (long long)((ka.m + 255) / 256) * ((ka.n + 255) / 256) * ka.batch;
+        if (t256 * 3 < num_cu)
+            return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
         launch_bs_pp(ka, MODE, OUT, stream);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;
@@ -285,10 +299,6 @@ static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
     // Up to 64 rows: the B-streaming kernel (gemm_bs_decode.hip), unless
     // 33-64 rows leave this file's 64x256 tile enough workgroups (a quarter
     // of the CUs): then its A reuse across 256 columns wins.
-    int num_cu = 0;
-    ga_status st = device_cu_count(&num_cu);
-    if (st != GA_OK)
-        return st;
     const long long tiles = (long long)((ka.n + 255) / 256) * ka.batch;
     if (ka.m > 32 && tiles * 4 >= num_cu)
         return launch_bs<BsCfg<64, 256, 1, 4, MODE, OUT>>(ka, stream);

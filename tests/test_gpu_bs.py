@@ -55,7 +55,11 @@ def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
                                    (16, 1000, 2048), (64, 7168, 1024), (8, 3000, 1536),
                                    (1, 8200, 4096),
                                    # ... or the 64x256 tile when it has enough tiles
-                                   (40, 16640, 256)])
+                                   (40, 16640, 256),
+                                   # more rows: the 128x128 tile while 256x256 tiles
+                                   # would cover less than a third of the CUs (all the
+                                   # shapes above with M > 64), the 256x256 kernel here
+                                   (1024, 7168, 256)])
 def test_blockscale(dev, group_n, shape):
     M, N, K = shape
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + N, group_n=group_n)
@@ -74,6 +78,31 @@ def test_blockscale(dev, group_n, shape):
     assert np.max(np.abs(got - ref)) <= 2e-4 * max(1.0, float(np.max(np.abs(ref))))
     Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, group_n)
     gb = Cb[0].view(torch.int16).cpu().numpy().view(np.uint16)
+    ok, st = bf16_compare(gb, oracle.to_bf16_bits(want), absdot)
+    assert st["bad"] == 0
+
+
+@pytest.mark.parametrize("shape", [(4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)])
+def test_blockscale_deepseek_configs(dev, shape):
+    """The DeepSeek shapes the benchmark configuration names, run whole on the
+    GPU (fp32 and bf16 C) and checked on 40 rows: the first and last 8 and 24
+    spread between (the CPU oracle on every row would take minutes)."""
+    M, N, K = shape
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=17)
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(M - 8, M),
+                                     np.linspace(8, M - 9, 24).astype(np.int64)]))
+    qa_r = np.ascontiguousarray(qa[0][rows])
+    sfa_r = np.ascontiguousarray(sfa[0][:, rows])
+    want = oracle.gemm_blockscale_fp32acc(qa_r, qb[0], sfa_r, sfb[0], 128)
+    absdot = oracle.blockscale_absdot(qa_r, qb[0], sfa_r, sfb[0], 128)
+    C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
+    ok, st = f32_compare(C[0].cpu().numpy()[rows], want, absdot=absdot)
+    print("bs f32 %s: exact=%.5f max_ulp=%d bounded=%d bad=%d" % (
+        shape, st["exact"], st["max_ulp"], st["bounded"], st["bad"]), flush=True)
+    assert st["bad"] == 0
+    del C
+    Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, 128)
+    gb = Cb[0].view(torch.int16).cpu().numpy().view(np.uint16)[rows]
     ok, st = bf16_compare(gb, oracle.to_bf16_bits(want), absdot)
     assert st["bad"] == 0
 
@@ -101,7 +130,8 @@ def test_blockscale_batched_small_m(dev):
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 512), (200, 1040, 1024), (1, 512, 256),
-                                   (600, 1000, 768), (16, 4000, 2048), (48, 600, 1024)])
+                                   (600, 1000, 768), (16, 4000, 2048), (48, 600, 1024),
+                                   (1024, 7168, 256)])
 def test_per_tensor(dev, shape):
     M, N, K = shape
     xa = oracle.randn(M * K, 11).reshape(M, K)
