@@ -188,6 +188,67 @@ __device__ __forceinline__ void a16_store_c(const ga_flatmm_splitk_kargs& ka, in
     }
 }
 
+// Writes acc as the fp32 partials of slice `split`.
+template <class C>
+__device__ __forceinline__ void a16_store_ws(const ga_flatmm_splitk_kargs& ka, float* ws, int split,
+                                             int b, int m0, int n0, int wm, int wn, int lane,
+                                             const v4f (&acc)[C::TM][C::TN])
+{
+    const size_t split_stride = (size_t)ka.batch * (size_t)ka.stride_ws_batch;
+    float* wsb = ws + (size_t)b * (size_t)ka.stride_ws_batch;
+    const bool vec = (ka.stride_ws & 3) == 0 && ((uintptr_t)ws & 15) == 0 &&
+                     (ka.stride_ws_batch & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
+        const int m = m0 + wm * C::WTM + i * 16 + (lane & 15);
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int n = n0 + wn * C::WTN + j * 16 + (lane >> 4) * 4;
+            if (m >= ka.m || n >= ka.n)
+                continue;
+            float* o = wsb + split * split_stride + (size_t)m * ka.stride_ws + n;
+            if (vec && n + 4 <= ka.n) {
+                *(v4f*)o = acc[i][j];
+            } else {
+                for (int e = 0; e < 4 && n + e < ka.n; e++)
+                    o[e] = acc[i][j][e];
+            }
+        }
+    }
+}
+
+// Workgroup -> (slice, M tile, N tile): XCD round-robin undone (each XCD gets
+// a contiguous range), slice outermost, then M-grouped tiles.
+__device__ __forceinline__ void a16_map(int tiles_m, int tiles_n, int& split, int& tm, int& tn)
+{
+    int lin = blockIdx.x;
+    const int total = gridDim.x;
+    const int full = (total / 8) * 8;
+    if (lin < full)
+        lin = (lin % 8) * (total / 8) + lin / 8;
+    const int tiles = tiles_m * tiles_n;
+    split = lin / tiles;
+    const int t = lin - split * tiles;
+    const int per_group = kA16GroupM * tiles_n;
+    const int grp = t / per_group;
+    const int first_m = grp * kA16GroupM;
+    const int gsize = min(tiles_m - first_m, kA16GroupM);
+    const int r = t - grp * per_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+// The workspace of the handle, or null when it is missing or smaller than
+// the layout needs (the kernel then writes nothing).
+__device__ __forceinline__ float* a16_ws(const ga_flatmm_splitk_kargs& ka)
+{
+    const ga_splitk_ws_handle* h = ka.ws_handle;
+    float* ws = (float*)h->ptr;
+    const uint64_t need =
+        (uint64_t)ka.split_k * (uint64_t)ka.batch * (uint64_t)ka.stride_ws_batch * 4u;
+    return (ws == nullptr || h->bytes < need) ? nullptr : ws;
+}
+
 template <class C, int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
 void a16w16_splitk_kernel(A16Args p)
@@ -200,30 +261,15 @@ void a16w16_splitk_kernel(A16Args p)
     const int wm = wave >> 1, wn = wave & 1;
     const int M = ka.m, N = ka.n, K = ka.k;
 
-    int lin = blockIdx.x;
-    const int total = gridDim.x;
-    const int full = (total / 8) * 8;
-    if (lin < full)
-        lin = (lin % 8) * (total / 8) + lin / 8;
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int split = lin / tiles;
-    const int t = lin - split * tiles;
-    const int per_group = kA16GroupM * p.tiles_n;
-    const int grp = t / per_group;
-    const int first_m = grp * kA16GroupM;
-    const int gsize = min(p.tiles_m - first_m, kA16GroupM);
-    const int r = t - grp * per_group;
-    const int m0 = (first_m + r % gsize) * C::BM;
-    const int n0 = (r / gsize) * C::BN;
+    int split, tm, tn;
+    a16_map(p.tiles_m, p.tiles_n, split, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int b = blockIdx.z;
 
     float* ws = nullptr;
     if (EPI != EPI_C) {
-        const ga_splitk_ws_handle* h = ka.ws_handle;
-        ws = (float*)h->ptr;
-        const uint64_t need =
-            (uint64_t)ka.split_k * (uint64_t)ka.batch * (uint64_t)ka.stride_ws_batch * 4u;
-        if (ws == nullptr || h->bytes < need)
+        ws = a16_ws(ka);
+        if (ws == nullptr)
             return;
     }
 
@@ -303,27 +349,7 @@ void a16w16_splitk_kernel(A16Args p)
         a16_store_c<C>(ka, b, m0, n0, wm, wn, lane, acc);
         return;
     }
-    const size_t split_stride = (size_t)ka.batch * (size_t)ka.stride_ws_batch;
-    float* wsb = ws + (size_t)b * (size_t)ka.stride_ws_batch;
-    const bool vec = (ka.stride_ws & 3) == 0 && ((uintptr_t)ws & 15) == 0 &&
-                     (ka.stride_ws_batch & 3) == 0;
-#pragma unroll
-    for (int i = 0; i < C::TM; i++) {
-        const int m = m0 + wm * C::WTM + i * 16 + (lane & 15);
-#pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const int n = n0 + wn * C::WTN + j * 16 + (lane >> 4) * 4;
-            if (m >= M || n >= N)
-                continue;
-            float* o = wsb + split * split_stride + (size_t)m * ka.stride_ws + n;
-            if (vec && n + 4 <= N) {
-                *(v4f*)o = acc[i][j];
-            } else {
-                for (int e = 0; e < 4 && n + e < N; e++)
-                    o[e] = acc[i][j][e];
-            }
-        }
-    }
+    a16_store_ws<C>(ka, ws, split, b, m0, n0, wm, wn, lane, acc);
 }
 
 // One configuration over split_k x tiles workgroups (x) and batch (z).
@@ -347,7 +373,9 @@ static ga_status launch_a16(const ga_flatmm_splitk_kargs& ka, int kslice, hipStr
 // Tile configurations, largest first. Measured on MI355X (bf16, 2048-8192
 // sized problems and the skinny 1024x512x7168): the largest tile whose grid
 // still gives every CU a workgroup wins; 128-row tiles are not used for M up
-// to 64 (they would compute mostly padding).
+// to 64 (they would compute mostly padding). B loaded straight into
+// registers (as the preshuffled MX kernels do) was measured slower here: a
+// row-major B fragment load touches 16 rows x 64 bytes per instruction.
 typedef A16Cfg<128, 256, 3> A16Huge;
 typedef A16Cfg<128, 128, 4> A16Big;
 typedef A16Cfg<64, 128, 4> A16Mid;
@@ -387,8 +415,8 @@ static ga_status check_a16(const ga_flatmm_splitk_kargs* ka)
     if (ka->stride_a < ka->k || ka->stride_b < ka->k || ka->stride_a % 8 || ka->stride_b % 8)
         return fail(GA_ERR_SHAPE, "a16w16 split-K: stride_a/stride_b must be >= K and "
                                   "multiples of 8");
-    if (ka->stride_a > (1 << 23) || ka->stride_b > (1 << 23))
-        return fail(GA_ERR_SHAPE, "a16w16 split-K: row stride above 2^23 elements");
+    if (ka->stride_a > (1 << 22) || ka->stride_b > (1 << 22))
+        return fail(GA_ERR_SHAPE, "a16w16 split-K: row stride above 2^22 elements");
     if (((uintptr_t)ka->ptr_a & 15) || ((uintptr_t)ka->ptr_b & 15))
         return fail(GA_ERR_ARG, "a16w16 split-K: A and B must be 16-byte aligned");
     if (ka->stride_a_batch < 0 || ka->stride_b_batch < 0 || ka->stride_c_batch < 0)

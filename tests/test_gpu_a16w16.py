@@ -68,6 +68,14 @@ SHAPES = [
     (2048, 1536, 1024, 2),  # 128x128 tiles
     (2048, 2048, 1000, 2),  # 128x256 tiles, K tail
     (520, 1000, 1024, 4),   # 64x128 tiles, ragged M and N
+    # few rows (64-row tiles over mostly zero rows), wide N
+    (16, 7168, 2048, 1),
+    (48, 3000, 1000, 2),    # N % 16 == 8, K tail
+    (8, 65536, 256, 2),     # 64x128 tiles
+    (64, 8192, 512, 4),     # 64x128 tiles
+    (33, 520, 4104, 3),     # 8-element K tail in the last slice
+    (24, 16384, 512, 2),
+    (40, 32768, 256, 2),
 ]
 
 
