@@ -323,7 +323,9 @@ size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N
  * summed in fp32 in `workspace` (ga_kernel_workspace_bytes) and a reduce
  * kernel writes bf16 D; D need not be pre-zeroed. workspace == NULL with
  * gdz > 1 uses a library-owned per-device buffer (grown on demand; not safe
- * to capture into a HIP graph). */
+ * to capture into a HIP graph). Every such call on a device shares that
+ * buffer: split-K launches on different streams that overlap in time race
+ * on it, so concurrent callers pass their own workspace. */
 ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
                            int gdz, void* workspace, size_t workspace_bytes,
                            void* stream);
