@@ -602,17 +602,17 @@ static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy,
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp8_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 32, 8}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS>>, 64, 8}
 // Preshuffled-B entries with 32 or 64 rows run the B-streaming tile (IBN
 // columns per workgroup, 4 steps in flight).
 #define GA_MXB_ENTRY(BM, BN, IBN, SPLIT, SUFFIX)                                               \
     {{BM, BN, SPLIT, 1, "ga_mxfp8_bf16_BpreShuffle_" #BM "x" #BN SUFFIX,                      \
       "ga_mxfp8_bf16_BpreShuffle_" #BM "x" #BN SUFFIX ".co"},                                 \
-     &launch_mxb<MbCfg<BM, IBN, 4, false>>, 32, 8}
+     &launch_mxb<MbCfg<BM, IBN, 4, false>>, 64, 8}
 #define GA_MX4B_ENTRY(BM, BN, IBN, SPLIT, SUFFIX)                                              \
     {{BM, BN, SPLIT, 1, "ga_mxfp4_bf16_BpreShuffle_" #BM "x" #BN SUFFIX,                      \
       "ga_mxfp4_bf16_BpreShuffle_" #BM "x" #BN SUFFIX ".co"},                                 \
-     &launch_mxb<MbCfg<BM, IBN, 4, true>>, 32, 4}
+     &launch_mxb<MbCfg<BM, IBN, 4, true>>, 64, 4}
 #define GA_BPS_NAME_1 "BpreShuffle"
 #define GA_BPS_NAME_0 "noBpreShuffle"
 
@@ -628,7 +628,7 @@ static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy,
     {{BM, BN, SPLIT, BPS,                                                                     \
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX,                              \
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_" #BM "x" #BN SUFFIX ".co"},                       \
-     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS, true>>, 32, 4}
+     &launch_mx<MxCfg<BM, BN, WGM, WGN, (BPS != 0), NS, true>>, 64, 4}
 #define GA_MX4_PP_ENTRY(BPS, SPLIT, SUFFIX, FN)                                                \
     {{256, 256, SPLIT, BPS, "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX,               \
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
@@ -777,6 +777,11 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
             return fail(GA_ERR_ARG, "gdz=%d does not match log2_k_split=%d", gdz, L);
     }
     hipStream_t s = (hipStream_t)stream;
+    // a caller workspace is checked against ga_kernel_workspace_bytes whichever
+    // path runs (the decode path sums K slices in LDS and needs none)
+    if (gdz > 1 && workspace && workspace_bytes < (size_t)gdz * M * N * sizeof(float))
+        return fail(GA_ERR_WORKSPACE, "workspace %zu bytes, need %zu", workspace_bytes,
+                    (size_t)gdz * M * N * sizeof(float));
     if ((int)args->M <= k.small_m_stream && mx_decode_applies(*args, gdz)) {
         // few rows: stream B, K slices summed inside the kernel (no workspace)
         int num_cu = 0;
@@ -791,10 +796,7 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
     if (gdz > 1) {
         size_t need = (size_t)gdz * M * N * sizeof(float);
         if (workspace) {
-            if (workspace_bytes < need)
-                return fail(GA_ERR_WORKSPACE, "workspace %zu bytes, need %zu", workspace_bytes,
-                            need);
-            ws = (float*)workspace;
+            ws = (float*)workspace; // size checked above
         } else {
             void* p = nullptr;
             ga_status st = default_workspace(need, &p);

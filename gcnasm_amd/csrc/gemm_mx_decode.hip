@@ -1,7 +1,8 @@
 // gemm_mx_decode.hip -- MXFP8 GEMM for small M (decode), HBM-streaming.
 //
-// Used by the manifest kernels for M <= 64 rows (256x256) or M <= 32 (the
-// other tiles, whose own grid wins for 33-64 rows): with so few rows the GEMM
+// Used by every manifest kernel for M <= 64 rows (measured on MI355X: for
+// 33-64 rows the tiles' own grids cover too few CUs, e.g. M = 48, N = 8192,
+// K = 28672 on 256x128: 215 us, here 70 us): with so few rows the GEMM
 // is a stream over B (N x K bytes), so the design is about keeping HBM busy:
 //  * one wave per NG 16-column groups of B and one K slice; B's 2 KB per
 //    group and 128-K step (two 1 KB contiguous runs in the preshuffled
