@@ -788,6 +788,20 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         ga_status st = device_cu_count(&num_cu);
         if (st != GA_OK)
             return st;
+        // 33-64 rows over wide N (32x256 B-streaming tiles covering 3/4 of
+        // the CUs): those tiles load A once per 256 columns where the decode
+        // kernel's waves load it per 32 (measured on MI355X, M = 64,
+        // N = 28672, K = 8192: 75.8 -> 38.9 us MXFP8, 41.5 -> 23.8 us MXFP4;
+        // with fewer tiles the decode kernel's K slices win)
+        const long long wide = (long long)((M + 31) / 32) * ((N + 255) / 256);
+        if (gdz == 1 && M > 32 && k.cfg.bpreshuffle && wide * 4 >= 3LL * num_cu) {
+            if (k.elem_bits == 4)
+                launch_mxb<MbCfg<32, 256, 4, true>>(*args, nullptr, 0, (M + 31) / 32, 1, s);
+            else
+                launch_mxb<MbCfg<32, 256, 4, false>>(*args, nullptr, 0, (M + 31) / 32, 1, s);
+            GA_HIP_CHECK(hipGetLastError());
+            return GA_OK;
+        }
         launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, num_cu, s);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;

@@ -233,6 +233,22 @@ def test_decode_path(dev, M, NKL):
           (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
+@pytest.mark.parametrize("M", [33, 64])
+@pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x128_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_32x512_splitK"])
+def test_few_rows_wide_n(dev, M, name):
+    """33-64 rows over N wide enough for 32x256 B-streaming tiles on 3/4 of
+    the CUs (the path ga_kernel_launch takes there instead of the decode
+    kernel), N not a multiple of 256."""
+    N, K = 28672 - 16, 512
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M + 3, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, 0)
+    assert ld.gdz == 1
+    check(got, expect(qa, sa, qb, sb, 0), "few rows wide N M=%d %s" % (M, name),
+          oracle.mx_absdot(qa, sa, qb, sb))
+
+
 @pytest.mark.parametrize("M", [1, 40])
 def test_decode_path_plain_b_and_epilogue(dev, M):
     """Row-major B and alpha/beta through the small-M path."""

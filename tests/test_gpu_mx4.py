@@ -135,6 +135,16 @@ def test_fp4_decode_path(dev, M, NKL):
     check4(got, qa, sa, qb, sb, l2, "decode M=%d N=%d K=%d L=%d" % (M, N, K, l2))
 
 
+@pytest.mark.parametrize("M", [33, 64])
+def test_fp4_few_rows_wide_n(dev, M):
+    """33-64 rows over wide N run 32x256 B-streaming tiles instead of the
+    decode kernel."""
+    N, K = 28672 - 16, 512
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + 5)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_BpreShuffle_256x128_splitK"), 0)
+    check4(got, qa, sa, qb, sb, 0, "few rows wide N M=%d" % M)
+
+
 def test_fp4_decode_plain_b(dev):
     M, N, K = 16, 1024, 2048
     qa, sa, qb, sb = mx4_operands(M, N, K, seed=77)
