@@ -9,9 +9,11 @@ C ABI (select_kernel -> make_launch -> fill_args -> kernel launch). Inputs are
 synthetic: N(0,1) values scaled by 2^u per 1x32 block (u uniform in [-4, 4]),
 quantised on the GPU by the library's MX quantiser (scale rule floor(log2(amax/448))).
 
-Also measured (reported in "decode"): the decode GEMMs M=16, N=28672, K=8192
-and M=16, N=8192, K=28672 with weights from N(0, 0.02), rotating 3 weight sets
-(> 256 MB Infinity Cache), at the reference driver's default log2_k_split=0.
+Also measured (reported in "decode" and "decode_other"): the decode GEMMs
+M=16, N=28672, K=8192 and M=16, N=8192, K=28672, then the same at M=1 and
+M=64 (the configuration's M in {1, 16, 64}), with weights from N(0, 0.02),
+rotating 3 weight sets (> 256 MB Infinity Cache), at the reference driver's
+default log2_k_split=0.
 
 "mxfp4" / "mxfp4_decode" run the same two workloads with OCP e2m1 operands.
 The reference's own f4gemm kernels are MXFP4; its published table
@@ -457,7 +459,8 @@ def main():
     # first, on an idle GPU: right after the MFMA-heavy legs the power
     # controller leaves the memory path a few percent slower for about a second.
     decode = []
-    for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672)):
+    for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672), (1, 28672, 8192),
+                       (1, 8192, 28672), (64, 28672, 8192), (64, 8192, 28672)):
         da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=1)
         dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30), args.warmup,
                        log2_k_split=0)
