@@ -13,14 +13,15 @@
 // through the buffer range check; a partial last N group of 128 is fine).
 // C is fp32 (the reference's output type) or bf16.
 //
-// 33-64 rows with enough columns, or more rows with few 256x256 tiles (this
-// file): 4 waves, 64x256 or 128x128 tile, K step 128, A and B
+// 33-64 rows with enough columns, or more rows whose 128x128 tiles fit on
+// the CUs in one round (this file): 4 waves, 64x256 or 128x128 tile, K step
+// 128, three LDS stages, A and B
 // staged with buffer_load ... lds (8 whole 128-byte rows per instruction)
 // into swizzled LDS rows (chunk c of row r at slot c ^ ((r >> 1) & 7)),
 // v_mfma_scale_f32_16x16x128_f8f6f4 with unit E8M0 scales (127) and the
 // operands swapped so a lane owns 4 consecutive N of one C row. More rows go
-// to the 256x256 eight-wave kernel of gemm_bs_pp.hip when its grid covers a
-// third of the CUs, fewer rows (or too few 256-column tiles) to the
+// to the 256x256 eight-wave kernel of gemm_bs_pp.hip, fewer rows (or too
+// few 256-column tiles) to the
 // B-streaming kernel of gemm_bs_decode.hip.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
@@ -40,7 +41,8 @@ struct BsCfg {
     static constexpr int TM = WTM / 16, TN = WTN / 16;
     static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS = 2 * STAGE;
+    static constexpr int NS = 3; // LDS stages: two in flight while one is computed
+    static constexpr int LDS = NS * STAGE;
     static constexpr int A_LOADS = A_BYTES / (NT * 16);
     static constexpr int B_LOADS = B_BYTES / (NT * 16);
     static constexpr int SB_PER_TILE = MODE == BS_GROUP1 ? 4 : 1;
@@ -189,38 +191,41 @@ void bs_gemm_kernel(ga_opus_gemm_kargs ka, int tiles_n)
         }
     };
 
-    // K loop: pairs of 128-K steps (stage 0 then stage 1) and an optional
-    // tail step in stage 0. The next stage is issued unconditionally so the
-    // body has no branch: past the last group the LDS loads read in-bounds
-    // bytes that are never used or range-checked zeros, and the scale group
-    // index is clamped to the last group.
+    // K loop over three LDS stages. Step s waits for its copies and scales
+    // (counted vmcnt: only the copies of step s+1 are younger), then, after
+    // the barrier that frees the buffer step s-1 used, loads the scales of
+    // step s+1 and copies step s+2 (in that order, so the next wait leaves
+    // exactly one step of copies in flight), then computes step s. Two scale
+    // sets alternate (the loop is unrolled by two). Copies past the last
+    // group read in-bounds bytes that are never used or range-checked zeros;
+    // the scale group index is clamped to the last group.
     const int nsteps = K / 128;
-    const int npairs = nsteps >> 1;
-    BsScales<C> cur, nxt;
+    constexpr int TL = C::A_LOADS + C::B_LOADS;
+    BsScales<C> sc0, sc1;
     issue(0, 0);
-    load_scales(0, cur);
-    for (int p = 0; p < npairs; p++) {
-        const int s = 2 * p;
-        wait_vmcnt<0>();
-        __syncthreads();
-        issue(1, (s + 1) * 128);
-        load_scales(s + 1, nxt);
+    load_scales(0, sc0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, 128);
+    int buf = 0; // LDS buffer of step s
+    auto step = [&](int s, const BsScales<C>& cur, BsScales<C>& nxt) {
+        wait_vmcnt<TL>();
+        barrier_lds();
+        load_scales(min(s + 1, nsteps - 1), nxt);
         __builtin_amdgcn_sched_barrier(0);
-        compute(0, cur);
+        issue(buf == 0 ? 2 : buf - 1, (s + 2) * 128);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<0>();
-        __syncthreads();
-        issue(0, (s + 2) * 128);
-        load_scales(min(s + 2, nsteps - 1), cur);
+        compute(buf, cur);
         __builtin_amdgcn_sched_barrier(0);
-        compute(1, nxt);
-        __builtin_amdgcn_sched_barrier(0);
+        buf = buf == 2 ? 0 : buf + 1;
+    };
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        step(s, sc0, sc1);
+        step(s + 1, sc1, sc0);
     }
-    if (nsteps & 1) {
-        wait_vmcnt<0>();
-        __syncthreads();
-        compute(0, cur);
-    }
+    if (s < nsteps)
+        step(s, sc0, sc1);
+    wait_vmcnt<0>(); // copies past the last group land before exit
 
     float tscale = 1.0f;
     if constexpr (C::MODE == BS_TENSOR)
@@ -283,14 +288,14 @@ static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
     if (st != GA_OK)
         return st;
     // More than 64 rows: the 256x256 eight-wave kernel (gemm_bs_pp.hip), or
-    // this file's 128x128 tile when 256x256 tiles would cover less than a
-    // third of the CUs (measured on MI355X, fp32 C: 512x7168x2048 35.4 ->
-    // 23.5 us, 1024x4096x4096 54.9 -> 39.8 us; with 112 or more 256x256
-    // tiles the eight-wave kernel is faster).
+    // this file's 128x128 tile when its tiles fit on the CUs in one round
+    // (measured on MI355X, fp32 C: 512x7168x2048 35.4 -> 18.8 us,
+    // 512x2112x7168 86.1 -> 43.7 us, 1024x4096x4096 54.9 -> 29.7 us; with a
+    // second round, e.g. 768x7168x2048, the eight-wave kernel is faster).
     if (ka.m > 64) {
-        const long long t256 =
-            (long long)((ka.m + 255) / 256) * ((ka.n + 255) / 256) * ka.batch;
-        if (t256 * 3 < num_cu)
+        const long long t128 =
+            (long long)((ka.m + 127) / 128) * ((ka.n + 127) / 128) * ka.batch;
+        if (t128 <= num_cu)
             return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
         launch_bs_pp(ka, MODE, OUT, stream);
         GA_HIP_CHECK(hipGetLastError());

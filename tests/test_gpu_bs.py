@@ -56,9 +56,9 @@ def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
                                    (1, 8200, 4096),
                                    # ... or the 64x256 tile when it has enough tiles
                                    (40, 16640, 256),
-                                   # more rows: the 128x128 tile while 256x256 tiles
-                                   # would cover less than a third of the CUs (all the
-                                   # shapes above with M > 64), the 256x256 kernel here
+                                   # more rows: the 128x128 tile while its tiles fit on
+                                   # the CUs in one round (all the shapes above with
+                                   # M > 64), the 256x256 kernel here
                                    (1024, 7168, 256)])
 def test_blockscale(dev, group_n, shape):
     M, N, K = shape
