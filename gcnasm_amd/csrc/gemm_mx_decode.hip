@@ -26,21 +26,24 @@
 namespace ga {
 namespace {
 
-template <int TM, int NG_>
+// DEEP: up to 4 waves per workgroup, so each may use 512 registers and keep
+// 4 steps of 64 rows in flight (for long K with one column task per CU).
+template <int TM, int NG_, bool DEEP = false>
 struct DecCfg {
     static constexpr int NG = NG_; // 16-column groups per wave
-    static constexpr int D = TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
+    static constexpr int D = DEEP ? 4 : TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
+    static constexpr int MAX_WAVES = DEEP ? 4 : 8;
 };
 
 // Uniform byte offsets as SGPR operands.
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-template <int TM, int NG_, bool BPS, bool FP4>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, 512)))
+template <int TM, int NG_, bool BPS, bool FP4, bool DEEP>
+__global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP>::MAX_WAVES * 64)))
 void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
 {
     constexpr int kEPB = FP4 ? 2 : 1; // elements per byte
-    constexpr int D = DecCfg<TM, NG_>::D, NG = NG_, NB = NG; // one scale dword per group
+    constexpr int D = DecCfg<TM, NG_, DEEP>::D, NG = NG_, NB = NG; // one scale dword per group
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
     constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
     static_assert(kLoadsPerStep * (D - 1) < 64, "vmcnt range");
@@ -244,18 +247,18 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
     }
 }
 
-// Workgroups: one per CU (more when a CU's share needs over 8 waves), each
-// with ceil(share / NG) column tasks x ks slices.
-template <int TM, int NG, bool BPS, bool FP4>
+// Workgroups: one per CU (more when a CU's share needs over MAX_WAVES
+// waves), each with ceil(share / NG) column tasks x ks slices (ks <= MAX_WAVES).
+template <int TM, int NG, bool BPS, bool FP4, bool DEEP = false>
 void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
-    const int max_tasks = 8 / ks; // waves per workgroup <= 8
+    const int max_tasks = DecCfg<TM, NG, DEEP>::MAX_WAVES / ks; // waves per workgroup
     int nwg = std::min(num_cu, (groups + NG - 1) / NG);
     nwg = std::max(nwg, (groups + NG * max_tasks - 1) / (NG * max_tasks));
     const int share = (groups + nwg - 1) / nwg;
     const int tasks = (share + NG - 1) / NG;
-    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4>), dim3(nwg), dim3(64 * tasks * ks), 0,
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP>), dim3(nwg), dim3(64 * tasks * ks), 0,
                        stream, args, nwg, ks);
 }
 
@@ -267,8 +270,22 @@ void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream
         launch_dec<1, 2, BPS, FP4>(args, gdz, num_cu, stream);
     else if (tm == 2)
         launch_dec<2, 2, BPS, FP4>(args, gdz, num_cu, stream);
-    else
-        launch_dec<4, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    else {
+        // 33-64 rows (measured on MI355X, MXFP8 / MXFP4 at M = 33 and 64):
+        // with at most one 16-column group per CU a wave per group
+        // (N = 4096, K = 4096: 12.1 -> 9.6 us MXFP8 at M = 33); with one
+        // two-group task per CU and long K, four steps in flight per wave
+        // (N = 8192, K = 28672: 67.9 -> 56.3 us MXFP8 at M = 33, 75.4 ->
+        // 69.1 at M = 64)
+        const int groups = (int)args.N / 16;
+        const int steps = (int)args.K / (FP4 ? 256 : 128) / gdz;
+        if (groups <= num_cu)
+            launch_dec<4, 1, BPS, FP4>(args, gdz, num_cu, stream);
+        else if (gdz <= 4 && steps >= 64 && (groups + 1) / 2 <= num_cu)
+            launch_dec<4, 2, BPS, FP4, true>(args, gdz, num_cu, stream);
+        else
+            launch_dec<4, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    }
 }
 
 } // namespace

@@ -233,6 +233,20 @@ def test_decode_path(dev, M, NKL):
           (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
+@pytest.mark.parametrize("MNK", [(40, 8192, 8192), (64, 8192, 8192), (64, 16384, 1024),
+                                 (48, 4096, 2048)])
+def test_decode_64_rows_paths(dev, MNK):
+    """33-64 rows in the decode kernel: four steps in flight with one two-group
+    task per CU and long K (N = 8192, K = 8192), eight waves of two groups
+    (N = 16384), one group per wave (N = 4096)."""
+    M, N, K = MNK
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_256x128_splitK")
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M + N, std_b=0.02)
+    got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0)
+    check(got, expect(qa, sa, qb, sb, 0), "decode 64-row path M=%d N=%d K=%d" % (M, N, K),
+          oracle.mx_absdot(qa, sa, qb, sb))
+
+
 @pytest.mark.parametrize("M", [33, 64])
 @pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x128_splitK",
                                   "ga_mxfp8_bf16_BpreShuffle_32x512_splitK"])

@@ -135,6 +135,15 @@ def test_fp4_decode_path(dev, M, NKL):
     check4(got, qa, sa, qb, sb, l2, "decode M=%d N=%d K=%d L=%d" % (M, N, K, l2))
 
 
+def test_fp4_decode_deep(dev):
+    """33-64 rows, one two-group task per CU and long K: the decode kernel
+    with four steps in flight."""
+    M, N, K = 40, 8192, 16384
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=77)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_BpreShuffle_256x128_splitK"), 0)
+    check4(got, qa, sa, qb, sb, 0, "decode deep M=%d N=%d K=%d" % (M, N, K))
+
+
 @pytest.mark.parametrize("M", [33, 64])
 def test_fp4_few_rows_wide_n(dev, M):
     """33-64 rows over wide N run 32x256 B-streaming tiles instead of the
