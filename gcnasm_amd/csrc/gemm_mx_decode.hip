@@ -27,11 +27,13 @@ namespace ga {
 namespace {
 
 // DEEP: up to 4 waves per workgroup, so each may use 512 registers and keep
-// 4 steps of 64 rows in flight (for long K with one column task per CU).
+// more steps in flight (4 of 64 rows, 6 of 32 rows; for long K with one
+// column task per CU).
 template <int TM, int NG_, bool DEEP = false>
 struct DecCfg {
     static constexpr int NG = NG_; // 16-column groups per wave
-    static constexpr int D = DEEP ? 4 : TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
+    static constexpr int D = DEEP ? (TM == 4 ? 4 : 6)
+                                  : TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
     static constexpr int MAX_WAVES = DEEP ? 4 : 8;
 };
 
@@ -268,8 +270,16 @@ void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream
     const int tm = ((int)args.M + 15) / 16;
     if (tm == 1)
         launch_dec<1, 2, BPS, FP4>(args, gdz, num_cu, stream);
-    else if (tm == 2)
-        launch_dec<2, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    else if (tm == 2) {
+        // 17-32 rows: six steps in flight for one two-group task per CU and
+        // long K, as for 64 rows below
+        const int groups = (int)args.N / 16;
+        const int steps = (int)args.K / (FP4 ? 256 : 128) / gdz;
+        if (gdz <= 4 && steps >= 64 && groups > num_cu && (groups + 1) / 2 <= num_cu)
+            launch_dec<2, 2, BPS, FP4, true>(args, gdz, num_cu, stream);
+        else
+            launch_dec<2, 2, BPS, FP4>(args, gdz, num_cu, stream);
+    }
     else {
         // 33-64 rows (measured on MI355X, MXFP8 / MXFP4 at M = 33 and 64):
         // with at most one 16-column group per CU a wave per group

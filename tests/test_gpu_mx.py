@@ -234,9 +234,9 @@ def test_decode_path(dev, M, NKL):
 
 
 @pytest.mark.parametrize("MNK", [(40, 8192, 8192), (64, 8192, 8192), (64, 16384, 1024),
-                                 (48, 4096, 2048)])
+                                 (48, 4096, 2048), (24, 8192, 8192)])
 def test_decode_64_rows_paths(dev, MNK):
-    """33-64 rows in the decode kernel: four steps in flight with one two-group
+    """17-64 rows in the decode kernel: more steps in flight with one two-group
     task per CU and long K (N = 8192, K = 8192), eight waves of two groups
     (N = 16384), one group per wave (N = 4096)."""
     M, N, K = MNK
