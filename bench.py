@@ -68,7 +68,10 @@ def parse():
     return ap.parse_args()
 
 
-def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0, elem_bits=8):
+def mx_inputs(torch, M, N, K, b_std=1.0, nsets=1, seed=0):
+    """The MX workloads' fp32 inputs, generated on the GPU: N(0,1) values
+    scaled by 2^u per 1x32 K-block (u uniform in [-4, 4]); B times b_std.
+    Returns (x_a [M, K], [x_b [N, K]] * nsets)."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -78,10 +81,23 @@ def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0, elem_bit
         u = torch.randint(-4, 5, (rows, K // 32, 1), device=dev, generator=g).float()
         return (x.view(rows, K // 32, 32) * torch.exp2(u)).view(rows, K)
 
+    xa = mx_input(M)
+    return xa, [mx_input(N) * b_std for _ in range(nsets)]
+
+
+def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0, elem_bits=8):
+    """mx_inputs quantised on the GPU (scale rule floor(log2(amax/448))) into
+    the kernel layout: A rows padded to 256, B 16x16-preshuffled, scales
+    padded and shuffled."""
     prep_a, prep_b = ((ops.prepare_mx_a, ops.prepare_mx_b) if elem_bits == 8 else
                       (ops.prepare_mx4_a, ops.prepare_mx4_b))
-    a = prep_a(mx_input(M))
-    bs = [prep_b(mx_input(N) * b_std) for _ in range(nsets)]
+    xa, xbs = mx_inputs(torch, M, N, K, b_std, nsets, seed)
+    a = prep_a(xa)
+    del xa
+    bs = []
+    for xb in xbs:
+        bs.append(prep_b(xb))
+    del xbs
     torch.cuda.synchronize()
     return a, bs
 
@@ -359,13 +375,20 @@ def a16w16_leg(torch, steps, warmup):
             "by_split_k": res}
 
 
+def scaled_inputs(torch, M, N, K, seed=2):
+    """fp32 inputs of the fp32-scale GEMM workloads: A [M, K], B [N, K] ~ N(0,1),
+    generated on the GPU."""
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(seed)
+    xa = torch.randn((M, K), device="cuda:0", generator=g)
+    xb = torch.randn((N, K), device="cuda:0", generator=g)
+    return xa, xb
+
+
 def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
     """DeepSeek block-scale (fp32 C) and per-tensor (bf16 C) GEMMs at 8192^3."""
     n = 8192
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(2)
-    xa = torch.randn((n, n), device="cuda:0", generator=g)
-    xb = torch.randn((n, n), device="cuda:0", generator=g)
+    xa, xb = scaled_inputs(torch, n, n, n)
     qa, sfa = ops.quant_fp8_1x128(xa)
     qb, sfb = ops.quant_fp8_128x128(xb)
     c = torch.empty((n, n), dtype=torch.float32, device="cuda:0")

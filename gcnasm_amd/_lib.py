@@ -198,11 +198,13 @@ SIGNATURES = {
     "ga_kernel_find": (_i, [ctypes.c_char_p, ctypes.POINTER(_i)]),
     "ga_kernel_workspace_bytes": (_sz, [_i, ctypes.POINTER(LaunchDesc), _i, _i]),
     "ga_kernel_launch": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _sz, _vp]),
+    "ga_kernel_launch_ws_handle": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _vp]),
     "ga_mxfp8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
                            ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
     "ga_mxfp4_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
                            ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
     "ga_gemm_a8w8_blockscale": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _i, _vp]),
+    "ga_blockscale_k_slices": (_i, [ctypes.POINTER(OpusGemmKargs), ctypes.POINTER(_i)]),
     "ga_fp8_gemm_per_tensor": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _vp]),
     "ga_splitk_reduce": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp]),
     "ga_splitk_reduce_ws_handle": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _i,

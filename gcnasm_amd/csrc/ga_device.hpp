@@ -9,6 +9,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include "../../include/gcnasm_amd.h"
 #include <stdint.h>
 
 #include <type_traits>
@@ -49,6 +51,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)up, (short)0,
                                              (int)__builtin_amdgcn_readfirstlane(bytes),
                                              0x00020000);
+}
+
+// Split-K workspace found through a device slot {ptr, bytes} at kernel entry
+// (graph-capture safe): the slot's buffer when it holds the [gdz, M, N] fp32
+// layout, else null (the caller then writes nothing).
+__device__ __forceinline__ float* resolve_ws(const ga_splitk_ws_handle* h, uint32_t gdz,
+                                             uint32_t M, uint32_t N)
+{
+    float* ws = (float*)h->ptr;
+    const uint64_t need = (uint64_t)gdz * M * N * 4u;
+    return (ws == nullptr || h->bytes < need) ? nullptr : ws;
 }
 
 // 16 bytes per lane from buffer `r` at byte offset voff+soff into LDS at

@@ -23,8 +23,11 @@ ga_status hip_fail(hipError_t e, const char* what);
     } while (0)
 
 // One compiled MX kernel: the manifest row plus its launcher.
-typedef void (*mx_launch_fn)(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy,
-                             int gdz, hipStream_t stream);
+// ws: the split-K workspace, or (wsh set) found through the device slot wsh at
+// kernel entry, where a slot shorter than the layout makes the kernel write nothing.
+typedef void (*mx_launch_fn)(const ga_f4gemm_kargs& args, float* ws,
+                             const ga_splitk_ws_handle* wsh, int gdx, int gdy, int gdz,
+                             hipStream_t stream);
 struct MxKernel {
     ga_tile_config cfg;
     mx_launch_fn launch;
@@ -32,15 +35,15 @@ struct MxKernel {
     int elem_bits;      // 8: E4M3 operands, 4: e2m1 packed two per byte
 };
 // 256x256 eight-wave kernels (gemm_mx_pp.hip), preshuffled / plain B.
-void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                      hipStream_t stream);
-void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                        hipStream_t stream);
+void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                      int gdx, int gdy, int gdz, hipStream_t stream);
+void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                        int gdx, int gdy, int gdz, hipStream_t stream);
 // The same tile for MXFP4 operands (e2m1, packed two per byte).
-void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                       hipStream_t stream);
-void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                         hipStream_t stream);
+void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                       int gdx, int gdy, int gdz, hipStream_t stream);
+void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                         int gdx, int gdy, int gdz, hipStream_t stream);
 // Small-M (decode) path shared by the kernels (gemm_mx_decode.hip): streams B
 // into registers, K slices summed in the workgroup (no workspace). Results
 // equal the tile kernels' (one fp32 chain of 128-K steps per slice).
@@ -57,11 +60,17 @@ void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStre
 // mode numbering.
 ga_status launch_bs_decode(const ga_opus_gemm_kargs& ka, int mode, int out_dtype,
                            hipStream_t stream);
+// 128-K groups per K slice of that kernel (slices are summed in order).
+int bs_decode_groups_per_slice(const ga_opus_gemm_kargs& ka, int num_cu);
 int mx_registry_count();  // MXFP8 manifest rows (registry entries [0, count))
 int mx_registry_total();  // every registry entry (manifests + kernels reachable by name)
 const MxKernel* mx_registry_get(int idx);
 int mx4_registry_first(); // MXFP4 manifest rows: entries [first, first + count)
 int mx4_registry_count();
+
+// Current bytes of a workspace slot made by ga_ws_handle_create (host mirror);
+// false for a slot the caller made itself.
+bool ws_slot_bytes(const ga_splitk_ws_handle* slot, size_t* bytes);
 
 // Library-owned per-device fp32 workspace, grown on demand.
 ga_status default_workspace(size_t bytes, void** ptr);

@@ -451,6 +451,20 @@ static std::unordered_map<const void*, WsSlot>& ws_slots()
     return m;
 }
 
+} // namespace ga
+
+bool ga::ws_slot_bytes(const ga_splitk_ws_handle* slot, size_t* bytes)
+{
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    auto it = ws_slots().find(slot);
+    if (it == ws_slots().end())
+        return false;
+    *bytes = it->second.bytes;
+    return true;
+}
+
+namespace ga {
+
 // Runs `f` with `dev` current, restoring the caller's device.
 template <class F>
 static ga_status on_device(int dev, F&& f)
@@ -474,11 +488,31 @@ using namespace ga;
 
 extern "C" {
 
+// A slot made by ga_ws_handle_create that holds less than the layout needs
+// (e.g. never reserved) is refused on the host when the stream is not
+// capturing; under capture (and for caller-made slots) the kernels' own
+// check applies: they write nothing.
+static ga_status check_ws_capacity(const ga_flatmm_splitk_kargs* ka, hipStream_t s)
+{
+    size_t have = 0;
+    const size_t need = ga_a16w16_splitk_workspace_bytes(ka);
+    if (!ws_slot_bytes(ka->ws_handle, &have) || have >= need)
+        return GA_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    GA_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return GA_OK;
+    return fail(GA_ERR_WORKSPACE, "a16w16 split-K: workspace slot holds %zu bytes, need %zu",
+                have, need);
+}
+
 ga_status ga_gemm_a16w16_flatmm_splitk(const ga_flatmm_splitk_kargs* kargs, void* stream)
 {
     ga_status st = check_a16(kargs);
     if (st == GA_OK)
         st = check_ws_layout(kargs);
+    if (st == GA_OK)
+        st = check_ws_capacity(kargs, (hipStream_t)stream);
     if (st != GA_OK)
         return st;
     return dispatch_a16<EPI_WS>(*kargs, (hipStream_t)stream);
@@ -507,6 +541,8 @@ ga_status ga_gemm_a16w16_splitk(const ga_flatmm_splitk_kargs* kargs, void* strea
     if (kargs->split_k == 1)
         return dispatch_a16<EPI_C>(*kargs, s);
     st = check_ws_layout(kargs);
+    if (st == GA_OK)
+        st = check_ws_capacity(kargs, s);
     if (st != GA_OK)
         return st;
     st = dispatch_a16<EPI_WS>(*kargs, s);

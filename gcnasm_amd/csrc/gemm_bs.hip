@@ -280,13 +280,10 @@ static ga_status launch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
     return GA_OK;
 }
 
-template <int MODE, int OUT>
-static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
+// Which kernel dispatch_bs runs for these kargs on a device with num_cu CUs.
+enum BsPath { BS_PATH_TILE128, BS_PATH_PP, BS_PATH_TILE64, BS_PATH_DECODE };
+static BsPath bs_path(const ga_opus_gemm_kargs& ka, int num_cu)
 {
-    int num_cu = 0;
-    ga_status st = device_cu_count(&num_cu);
-    if (st != GA_OK)
-        return st;
     // More than 64 rows: the 256x256 eight-wave kernel (gemm_bs_pp.hip), or
     // this file's 128x128 tile when its tiles fit on the CUs in one round
     // (measured on MI355X, fp32 C: 512x7168x2048 35.4 -> 18.8 us,
@@ -295,19 +292,36 @@ static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
     if (ka.m > 64) {
         const long long t128 =
             (long long)((ka.m + 127) / 128) * ((ka.n + 127) / 128) * ka.batch;
-        if (t128 <= num_cu)
-            return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
-        launch_bs_pp(ka, MODE, OUT, stream);
-        GA_HIP_CHECK(hipGetLastError());
-        return GA_OK;
+        return t128 <= num_cu ? BS_PATH_TILE128 : BS_PATH_PP;
     }
     // Up to 64 rows: the B-streaming kernel (gemm_bs_decode.hip), unless
     // 33-64 rows leave this file's 64x256 tile enough workgroups (a quarter
     // of the CUs): then its A reuse across 256 columns wins.
     const long long tiles = (long long)((ka.n + 255) / 256) * ka.batch;
     if (ka.m > 32 && tiles * 4 >= num_cu)
+        return BS_PATH_TILE64;
+    return BS_PATH_DECODE;
+}
+
+template <int MODE, int OUT>
+static ga_status dispatch_bs(const ga_opus_gemm_kargs& ka, hipStream_t stream)
+{
+    int num_cu = 0;
+    ga_status st = device_cu_count(&num_cu);
+    if (st != GA_OK)
+        return st;
+    switch (bs_path(ka, num_cu)) {
+    case BS_PATH_TILE128:
+        return launch_bs<BsCfg<128, 128, 2, 2, MODE, OUT>>(ka, stream);
+    case BS_PATH_PP:
+        launch_bs_pp(ka, MODE, OUT, stream);
+        GA_HIP_CHECK(hipGetLastError());
+        return GA_OK;
+    case BS_PATH_TILE64:
         return launch_bs<BsCfg<64, 256, 1, 4, MODE, OUT>>(ka, stream);
-    return launch_bs_decode(ka, MODE, OUT, stream);
+    default:
+        return launch_bs_decode(ka, MODE, OUT, stream);
+    }
 }
 
 static ga_status check_kargs(const ga_opus_gemm_kargs* ka)
@@ -324,6 +338,25 @@ static ga_status check_kargs(const ga_opus_gemm_kargs* ka)
         return fail(GA_ERR_SHAPE, "stride_c must be >= N");
     if (ka->batch > 65535)
         return fail(GA_ERR_SHAPE, "batch > 65535");
+    // operands are read through buffer descriptors based at a tile's first
+    // row, which address 4 GiB: 256 rows of A and B must fit in it
+    const unsigned long long lim = 0xFFFFFFF0ull;
+    if (256ull * (unsigned long long)ka->stride_a > lim ||
+        256ull * (unsigned long long)ka->stride_b > lim)
+        return fail(GA_ERR_SHAPE, "stride_a/stride_b too large for 32-bit buffer offsets "
+                                  "(256 rows must fit in 4 GiB)");
+    return GA_OK;
+}
+
+// The fp32 scale matrices are read through one descriptor each.
+static ga_status check_scales(const ga_opus_gemm_kargs* ka, int group_n)
+{
+    const unsigned long long lim = 0xFFFFFFF0ull, G = (unsigned long long)ka->k / 128;
+    const unsigned long long sfa = G * (unsigned long long)ka->stride_sfa * 4;
+    const unsigned long long sfb = (group_n == 128 ? ((unsigned long long)ka->n + 127) / 128 : G) *
+                                   (unsigned long long)ka->stride_sfb * 4;
+    if (sfa > lim || sfb > lim)
+        return fail(GA_ERR_SHAPE, "scale matrices larger than 4 GiB");
     return GA_OK;
 }
 
@@ -349,12 +382,32 @@ ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, 
         return fail(GA_ERR_SHAPE, "stride_sfb must be >= N for GROUP_N 1");
     if (kargs->stride_sfa < kargs->m)
         return fail(GA_ERR_SHAPE, "stride_sfa must be >= M (SFA is [K/128, M])");
+    st = check_scales(kargs, group_n);
+    if (st != GA_OK)
+        return st;
     hipStream_t s = (hipStream_t)stream;
     if (group_n == 128)
         return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_GROUP128, GA_DTYPE_F32>(*kargs, s)
                                          : dispatch_bs<BS_GROUP128, GA_DTYPE_BF16>(*kargs, s);
     return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_GROUP1, GA_DTYPE_F32>(*kargs, s)
                                      : dispatch_bs<BS_GROUP1, GA_DTYPE_BF16>(*kargs, s);
+}
+
+ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_per_slice)
+{
+    if (!kargs || !groups_per_slice)
+        return fail(GA_ERR_ARG, "ga_blockscale_k_slices: null argument");
+    if (kargs->m <= 0 || kargs->n <= 0 || kargs->k <= 0 || kargs->batch <= 0 ||
+        kargs->k % 128 != 0)
+        return fail(GA_ERR_SHAPE, "ga_blockscale_k_slices: M, N, K, batch > 0, K %% 128 == 0");
+    int num_cu = 0;
+    ga_status st = device_cu_count(&num_cu);
+    if (st != GA_OK)
+        return st;
+    *groups_per_slice = bs_path(*kargs, num_cu) == BS_PATH_DECODE
+                            ? bs_decode_groups_per_slice(*kargs, num_cu)
+                            : kargs->k / 128;
+    return GA_OK;
 }
 
 ga_status ga_fp8_gemm_per_tensor(const ga_opus_gemm_kargs* kargs, int out_dtype, void* stream)

@@ -272,15 +272,28 @@ void bs_decode_kernel(ga_opus_gemm_kargs ka, int nwg, int ks, int gps)
 // K slices: double while the waves stay within about four per CU and each
 // slice keeps at least two 128-K groups (at most 8 slices); workgroups take
 // equal shares of the column groups, at most 8 waves each.
+int bsd_ks(int n, int k, int ng, int num_cu)
+{
+    const int groups = (n + 15) / 16;
+    const int G = k / 128;
+    const int tasks_total = (groups + ng - 1) / ng;
+    int ks = 1;
+    while (ks < 8 && (long long)tasks_total * ks * 2 <= 4ll * num_cu && G / (ks * 2) >= 2)
+        ks *= 2;
+    return ks;
+}
+
+// one 16-column group per wave when there are fewer groups than CUs, so the
+// grid still reaches every CU; else two (A loads shared by two groups)
+int bsd_ng(int n, int num_cu) { return (n + 15) / 16 < num_cu ? 1 : 2; }
+
 template <int TM, int NG, int MODE, int OUT>
 ga_status launch_bsd(const ga_opus_gemm_kargs& ka, int num_cu, hipStream_t stream)
 {
     const int groups = (ka.n + 15) / 16;
     const int G = ka.k / 128;
     const int tasks_total = (groups + NG - 1) / NG;
-    int ks = 1;
-    while (ks < 8 && (long long)tasks_total * ks * 2 <= 4ll * num_cu && G / (ks * 2) >= 2)
-        ks *= 2;
+    const int ks = bsd_ks(ka.n, ka.k, NG, num_cu);
     const int gps = (G + ks - 1) / ks;
     const int max_tasks = 8 / ks;
     int nwg = std::min(num_cu, tasks_total);
@@ -297,9 +310,7 @@ template <int MODE, int OUT>
 ga_status launch_bsd_rows(const ga_opus_gemm_kargs& ka, int num_cu, hipStream_t stream)
 {
     const int tm = (ka.m + 15) / 16;
-    // one 16-column group per wave when there are fewer groups than CUs, so
-    // the grid still reaches every CU; else two (A loads shared by two groups)
-    const bool few = (ka.n + 15) / 16 < num_cu;
+    const bool few = bsd_ng(ka.n, num_cu) == 1;
     if (tm == 1)
         return few ? launch_bsd<1, 1, MODE, OUT>(ka, num_cu, stream)
                    : launch_bsd<1, 2, MODE, OUT>(ka, num_cu, stream);
@@ -311,6 +322,13 @@ ga_status launch_bsd_rows(const ga_opus_gemm_kargs& ka, int num_cu, hipStream_t 
 }
 
 } // namespace
+
+int bs_decode_groups_per_slice(const ga_opus_gemm_kargs& ka, int num_cu)
+{
+    const int G = ka.k / 128;
+    const int ks = bsd_ks(ka.n, ka.k, bsd_ng(ka.n, num_cu), num_cu);
+    return (G + ks - 1) / ks;
+}
 
 ga_status launch_bs_decode(const ga_opus_gemm_kargs& ka, int mode, int out_dtype,
                            hipStream_t stream)

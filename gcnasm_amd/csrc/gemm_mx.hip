@@ -236,9 +236,12 @@ __device__ __forceinline__ void mx_store(const ga_f4gemm_kargs& args, float* ws,
 
 template <class C>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(C::WPE, C::WPE)))
-void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
+void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws,
+                    const ga_splitk_ws_handle* __restrict__ wsh)
 {
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+    if (wsh && !(ws = resolve_ws(wsh, gridDim.z, args.M, args.N)))
+        return; // workspace slot shorter than the split-K layout: write nothing
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -377,10 +380,11 @@ void mx_gemm_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
 }
 
 template <class C>
-static void launch_mx(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                      hipStream_t stream)
+static void launch_mx(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                      int gdx, int gdy, int gdz, hipStream_t stream)
 {
-    hipLaunchKernelGGL(mx_gemm_kernel<C>, dim3(gdx, gdy, gdz), dim3(256), 0, stream, args, ws);
+    hipLaunchKernelGGL(mx_gemm_kernel<C>, dim3(gdx, gdy, gdz), dim3(256), 0, stream, args, ws,
+                       wsh);
 }
 
 // B-streaming tile for preshuffled B and few rows (BM = 32 or 64): the four
@@ -495,9 +499,12 @@ __device__ __forceinline__ void mb_compute(const char* smem, int buf, int step, 
 
 template <class C>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
-void mx_bstream_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
+void mx_bstream_kernel(ga_f4gemm_kargs args, float* __restrict__ ws,
+                       const ga_splitk_ws_handle* __restrict__ wsh)
 {
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+    if (wsh && !(ws = resolve_ws(wsh, gridDim.z, args.M, args.N)))
+        return; // workspace slot shorter than the split-K layout: write nothing
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
@@ -590,12 +597,13 @@ void mx_bstream_kernel(ga_f4gemm_kargs args, float* __restrict__ ws)
 // C::BN): the entry's grid fixes the tile a caller sees; a 32x512 workgroup
 // would leave half of the CUs idle at M <= 128.
 template <class C>
-static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                       hipStream_t stream)
+static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                       int gdx, int gdy, int gdz, hipStream_t stream)
 {
     (void)gdx;
     const int gx = ((int)args.N + C::BN - 1) / C::BN;
-    hipLaunchKernelGGL(mx_bstream_kernel<C>, dim3(gx, gdy, gdz), dim3(256), 0, stream, args, ws);
+    hipLaunchKernelGGL(mx_bstream_kernel<C>, dim3(gx, gdy, gdz), dim3(256), 0, stream, args, ws,
+                       wsh);
 }
 
 #define GA_MX_ENTRY(BM, BN, WGM, WGN, BPS, NS, SPLIT, SUFFIX)                                  \
@@ -734,8 +742,16 @@ size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N
     return (size_t)ld->gdz * M * N * sizeof(float);
 }
 
-ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
-                           void* workspace, size_t workspace_bytes, void* stream)
+} // extern "C"
+
+namespace ga {
+
+// ga_kernel_launch with the split-K workspace given either as a buffer
+// (workspace, workspace_bytes; NULL: the library-owned one) or as a device
+// slot read by the kernels at entry (wsh; graph-capture safe).
+static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
+                               void* workspace, size_t workspace_bytes,
+                               const ga_splitk_ws_handle* wsh, void* stream)
 {
     if (!args || idx < 0 || idx >= mx_registry_total())
         return fail(GA_ERR_ARG, "kernel_launch: bad kernel index %d", idx);
@@ -764,6 +780,22 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         args->stride_ScaleB0 < (uint32_t)(K / 32) || args->stride_ScaleB0 % 8)
         return fail(GA_ERR_SHAPE, "scale strides must be the padded column count "
                                   "round_up(K/32, 8)");
+    {
+        // Every kernel reads an operand through a buffer descriptor based at
+        // its tile's (or wave's) first row, which addresses 4 GiB: at most
+        // 512 rows of A or B, and the whole scale matrices, must fit in it.
+        const unsigned long long lim = 0xFFFFFFF0ull;
+        const unsigned long long ebits = (unsigned long long)k.elem_bits;
+        const unsigned long long lda = args->stride_A0 * ebits / 8;
+        const unsigned long long ldb = (k.cfg.bpreshuffle ? (unsigned long long)K
+                                                          : args->stride_B0) * ebits / 8;
+        const unsigned long long sa = ((unsigned long long)M + 255) / 256 * 256 * args->stride_ScaleA0;
+        const unsigned long long sb = ((unsigned long long)N + 255) / 256 * 256 * args->stride_ScaleB0;
+        if (512 * lda > lim || 512 * ldb > lim || sa > lim || sb > lim)
+            return fail(GA_ERR_SHAPE, "operand rows or scale matrices too large for 32-bit "
+                                      "buffer offsets (512 rows of A/B and each scale matrix "
+                                      "must fit in 4 GiB)");
+    }
     if (gdx != (N + k.cfg.tile_N - 1) / k.cfg.tile_N || gdy != (M + k.cfg.tile_M - 1) / k.cfg.tile_M ||
         gdz < 1)
         return fail(GA_ERR_ARG, "grid (%d,%d,%d) does not match tile %dx%d", gdx, gdy, gdz,
@@ -796,9 +828,9 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         const long long wide = (long long)((M + 31) / 32) * ((N + 255) / 256);
         if (gdz == 1 && M > 32 && k.cfg.bpreshuffle && wide * 4 >= 3LL * num_cu) {
             if (k.elem_bits == 4)
-                launch_mxb<MbCfg<32, 256, 4, true>>(*args, nullptr, 0, (M + 31) / 32, 1, s);
+                launch_mxb<MbCfg<32, 256, 4, true>>(*args, nullptr, nullptr, 0, (M + 31) / 32, 1, s);
             else
-                launch_mxb<MbCfg<32, 256, 4, false>>(*args, nullptr, 0, (M + 31) / 32, 1, s);
+                launch_mxb<MbCfg<32, 256, 4, false>>(*args, nullptr, nullptr, 0, (M + 31) / 32, 1, s);
             GA_HIP_CHECK(hipGetLastError());
             return GA_OK;
         }
@@ -807,11 +839,29 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         return GA_OK;
     }
     float* ws = nullptr;
-    if (gdz > 1) {
+    if (gdz > 1 && wsh) {
+        // the host mirror of a library-made slot catches a missing reserve
+        // outside capture; the kernels check the slot itself at every run
+        size_t have = 0;
+        if (ws_slot_bytes(wsh, &have) && have < (size_t)gdz * M * N * sizeof(float)) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            GA_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+            if (cs == hipStreamCaptureStatusNone)
+                return fail(GA_ERR_WORKSPACE, "workspace slot holds %zu bytes, need %zu", have,
+                            (size_t)gdz * M * N * sizeof(float));
+        }
+    } else if (gdz > 1) {
         size_t need = (size_t)gdz * M * N * sizeof(float);
         if (workspace) {
             ws = (float*)workspace; // size checked above
         } else {
+            // the library-owned buffer may be reallocated by a later call: a
+            // captured graph would keep a pointer that is then freed
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            GA_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+            if (cs != hipStreamCaptureStatusNone)
+                return fail(GA_ERR_WORKSPACE, "split-K launch under stream capture needs a "
+                                              "caller workspace");
             void* p = nullptr;
             ga_status st = default_workspace(need, &p);
             if (st != GA_OK)
@@ -819,12 +869,12 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
             ws = (float*)p;
         }
     }
-    k.launch(*args, ws, gdx, gdy, gdz, s);
+    k.launch(*args, ws, gdz > 1 ? wsh : nullptr, gdx, gdy, gdz, s);
     GA_HIP_CHECK(hipGetLastError());
     if (gdz > 1) {
         ReduceArgs r;
         r.ws = ws;
-        r.wsh = nullptr;
+        r.wsh = wsh;
         r.out = args->ptr_D;
         r.c_in = (args->beta != 0.0f) ? args->ptr_C : nullptr;
         r.bias = nullptr;
@@ -844,6 +894,24 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
         return splitk_reduce_launch(r, s);
     }
     return GA_OK;
+}
+
+} // namespace ga
+
+extern "C" {
+
+ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
+                           void* workspace, size_t workspace_bytes, void* stream)
+{
+    return kernel_launch(idx, args, gdx, gdy, gdz, workspace, workspace_bytes, nullptr, stream);
+}
+
+ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
+                                     int gdz, const ga_splitk_ws_handle* ws_handle, void* stream)
+{
+    if (gdz > 1 && !ws_handle)
+        return fail(GA_ERR_ARG, "kernel_launch_ws_handle: null workspace slot");
+    return kernel_launch(idx, args, gdx, gdy, gdz, nullptr, 0, ws_handle, stream);
 }
 
 ga_status ga_mxfp8_gemm(void* d_D, const void* d_A, const void* d_B, const void* d_ScaleA,

@@ -487,9 +487,12 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
 // are in flight, instead of behind a workgroup exit and a new launch.
 template <bool BPS, bool FP4>
 __global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
-void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws, int tiles_x, int tiles_y)
+void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws,
+                  const ga_splitk_ws_handle* __restrict__ wsh, int tiles_x, int tiles_y)
 {
     __shared__ __attribute__((aligned(1024))) char smem[kLds];
+    if (wsh && !(ws = resolve_ws(wsh, gridDim.z, args.M, args.N)))
+        return; // workspace slot shorter than the split-K layout: write nothing
     PpArgs a;
     a.ptr_A = uni_ptr(args.ptr_A);
     a.ptr_B = uni_ptr(args.ptr_B);
@@ -534,32 +537,32 @@ int pp_grid(int tiles)
 
 } // namespace
 
-void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                      hipStream_t stream)
+void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                      int gdx, int gdy, int gdz, hipStream_t stream)
 {
     hipLaunchKernelGGL((mx_pp_kernel<true, false>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
-                       0, stream, args, ws, gdx, gdy);
+                       0, stream, args, ws, wsh, gdx, gdy);
 }
 
-void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                        hipStream_t stream)
+void launch_mx_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                        int gdx, int gdy, int gdz, hipStream_t stream)
 {
     hipLaunchKernelGGL((mx_pp_kernel<false, false>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
-                       0, stream, args, ws, gdx, gdy);
+                       0, stream, args, ws, wsh, gdx, gdy);
 }
 
-void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                       hipStream_t stream)
+void launch_mx4_pp_bps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                       int gdx, int gdy, int gdz, hipStream_t stream)
 {
     hipLaunchKernelGGL((mx_pp_kernel<true, true>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
-                       0, stream, args, ws, gdx, gdy);
+                       0, stream, args, ws, wsh, gdx, gdy);
 }
 
-void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, int gdx, int gdy, int gdz,
-                         hipStream_t stream)
+void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                         int gdx, int gdy, int gdz, hipStream_t stream)
 {
     hipLaunchKernelGGL((mx_pp_kernel<false, true>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
-                       0, stream, args, ws, gdx, gdy);
+                       0, stream, args, ws, wsh, gdx, gdy);
 }
 
 } // namespace ga

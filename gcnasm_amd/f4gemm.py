@@ -231,7 +231,16 @@ class Kernel:
         d = ld.to_c()
         return lib().ga_kernel_workspace_bytes(self.idx, ctypes.byref(d), M, N)
 
-    def launch(self, args, gdx, gdy, gdz, stream=None, workspace=None):
+    def launch(self, args, gdx, gdy, gdz, stream=None, workspace=None, ws_handle=None):
+        """Kernel::launch. The split-K workspace is `workspace` (a tensor; None:
+        the library's own), or with `ws_handle` (a flatmm_splitk.WorkspaceHandle
+        or a device slot address) found through that slot when the kernels run
+        (ga_kernel_launch_ws_handle: safe to capture into a HIP graph)."""
+        if ws_handle is not None:
+            addr = getattr(ws_handle, "address", ws_handle)
+            check(lib().ga_kernel_launch_ws_handle(self.idx, ctypes.byref(args), gdx, gdy, gdz,
+                                                   addr, _stream_handle(stream)))
+            return
         ws_ptr, ws_bytes = None, 0
         if workspace is not None:
             ws_ptr = _ptr(workspace)

@@ -12,6 +12,15 @@ from ._lib import check, lib
 from .f4gemm import Shape, _stream_handle
 
 
+def _rows(x, what="x"):
+    """Checks that x is a [rows, K] matrix whose rows are contiguous (the
+    quantisers take a row stride, not a column stride)."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+        raise ValueError("%s must be a [rows, K] matrix with contiguous rows "
+                         "(shape %s, strides %s)" % (what, tuple(x.shape), tuple(x.stride())))
+    return x.shape
+
+
 def _in_dtype(x):
     if x.dtype == torch.float32:
         return _lib.GA_IN_F32
@@ -22,7 +31,7 @@ def _in_dtype(x):
 
 def quant_mxfp8(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
     """x [rows, K] -> (q uint8 [rows, K] E4M3, scales uint8 [rows, K/32] E8M0, unshuffled)."""
-    rows, K = x.shape
+    rows, K = _rows(x)
     q = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
     s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
     check(lib().ga_quant_mxfp8(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0), q.data_ptr(),
@@ -34,7 +43,7 @@ def quant_mxfp4(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
     """x [rows, K] -> (q uint8 [rows, K/2] packed e2m1, low nibble = even element;
     scales uint8 [rows, K/32] E8M0, unshuffled). Rule numbers as for MXFP8 with
     the e2m1 maximum 6 in place of 448."""
-    rows, K = x.shape
+    rows, K = _rows(x)
     q = torch.empty((rows, K // 2), dtype=torch.uint8, device=x.device)
     s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
     check(lib().ga_quant_mxfp4(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0), q.data_ptr(),
@@ -44,7 +53,7 @@ def quant_mxfp4(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
 
 def quant_fp8_1x128(x, stream=None):
     """x [rows, K] -> (q [rows, K], sfa fp32 [K/128, rows])."""
-    rows, K = x.shape
+    rows, K = _rows(x)
     q = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
     sfa = torch.empty((K // 128, rows), dtype=torch.float32, device=x.device)
     check(lib().ga_quant_fp8_1x128(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0),
@@ -55,7 +64,7 @@ def quant_fp8_1x128(x, stream=None):
 
 def quant_fp8_128x128(x, stream=None):
     """x [rows, K] -> (q [rows, K], sfb fp32 [ceil(rows/128), K/128])."""
-    rows, K = x.shape
+    rows, K = _rows(x)
     q = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
     sfb = torch.empty(((rows + 127) // 128, K // 128), dtype=torch.float32, device=x.device)
     check(lib().ga_quant_fp8_128x128(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0),
@@ -78,8 +87,9 @@ def quant_fp8_per_tensor(x, stream=None):
 
 def shuffle_weight_16x16(w, stream=None):
     """Device preshuffle of B [N, Kp] bytes (shuffle_weight(layout=(16,16)))."""
+    w = w.contiguous()
     N, Kp = w.shape
-    out = torch.empty_like(w)
+    out = torch.empty((N, Kp), dtype=w.dtype, device=w.device)
     check(lib().ga_shuffle_weight_16x16_device(w.data_ptr(), out.data_ptr(), N, Kp,
                                                _stream_handle(stream)))
     return out
@@ -87,6 +97,7 @@ def shuffle_weight_16x16(w, stream=None):
 
 def shuffle_scale(s, sm, sn, stream=None):
     """Device pad-to-[sm, sn] (0x7F) + shuffle of an E8M0 scale matrix [rows, cols]."""
+    s = s.contiguous()
     rows, cols = s.shape
     out = torch.empty((sm * sn,), dtype=torch.uint8, device=s.device)
     check(lib().ga_shuffle_scale_device(s.data_ptr(), out.data_ptr(), rows, cols, sm, sn,

@@ -83,3 +83,13 @@ def per_tensor_gemm(a, b, sa, sb, c, stream=None):
     ka = make_kargs(a, b, c, sa, sb, m, n, k, batch, group_n=0)
     fp8_gemm(ka, _out_dtype(c), stream)
     return c
+
+
+def k_slices(m, n, k, batch=1):
+    """128-K groups per K slice of the kernel these sizes run on the current
+    device (ga_blockscale_k_slices; K // 128 means one fp32 chain)."""
+    ka = opus_gemm_kargs()
+    ka.m, ka.n, ka.k, ka.batch = m, n, k, batch
+    g = ctypes.c_int(0)
+    check(lib().ga_blockscale_k_slices(ctypes.byref(ka), ctypes.byref(g)))
+    return g.value

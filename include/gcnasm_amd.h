@@ -322,13 +322,27 @@ size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N
  * strides still in elements, K % 256 == 0. With gdz > 1 the K-slices are
  * summed in fp32 in `workspace` (ga_kernel_workspace_bytes) and a reduce
  * kernel writes bf16 D; D need not be pre-zeroed. workspace == NULL with
- * gdz > 1 uses a library-owned per-device buffer (grown on demand; not safe
- * to capture into a HIP graph). Every such call on a device shares that
- * buffer: split-K launches on different streams that overlap in time race
- * on it, so concurrent callers pass their own workspace. */
+ * gdz > 1 uses a library-owned per-device buffer (grown on demand), and is
+ * refused with GA_ERR_WORKSPACE while `stream` is capturing a HIP graph.
+ * Every such call on a device shares that buffer: split-K launches on
+ * different streams that overlap in time race on it, so concurrent callers
+ * pass their own workspace. */
 ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
                            int gdz, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* ga_kernel_launch with the split-K workspace found through a device slot
+ * (ga_splitk_ws_handle, as the a16w16 split-K path takes it; no counterpart
+ * in asm_f4gemm, whose kernels add K slices with bf16 atomics): the GEMM
+ * kernels and the reduce read {ptr, bytes} from the slot when they run, so a
+ * captured HIP graph keeps working after ga_ws_handle_reserve grows the
+ * buffer. The slot must hold gdz * M * N floats (ga_kernel_workspace_bytes):
+ * for a slot made by ga_ws_handle_create this is checked on the host
+ * (GA_ERR_WORKSPACE) outside capture; a shorter slot met by the kernels makes
+ * them write nothing. gdz == 1 (and the M <= 64 paths) use no workspace. */
+ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
+                                     int gdz, const ga_splitk_ws_handle* ws_handle,
+                                     void* stream);
 
 /* One-call MXFP8 GEMM: select_kernel + make_launch + fill_args + launch.
  * log2_k_split as in ga_select_kernel. Writes the chosen kernel index and
@@ -363,6 +377,13 @@ ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n,
  * each point at one device fp32. B [N, K] K-major. */
 ga_status ga_fp8_gemm_per_tensor(const ga_opus_gemm_kargs* kargs, int out_dtype,
                                  void* stream);
+
+/* Summation order of the two calls above (no counterpart in the reference,
+ * whose kernel sums K in one chain): the kernel chosen for these kargs on the
+ * current device sums K in slices of *groups_per_slice 128-K groups, each
+ * slice in one fp32 chain, and adds the slices in order. K / 128 means one
+ * chain. Lets a caller (or a test) reproduce the rounding exactly. */
+ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_per_slice);
 
 /* splitk_reduce_kernel: C[b, m, n] = sum_s ws[s, b, m, n] (+ bias[n]) in fp32,
  * cast to out_dtype. ws is [split_k, batch, padded_M, padded_N] fp32. bias

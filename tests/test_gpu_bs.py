@@ -2,8 +2,10 @@
 
 Block-scale (DeepSeek 1x128 activation / 128x128 weight, and the 1x128x1
 per-column variant) and per-tensor. Expected values: the oracle's kernel-order
-fp32 accumulation (oracle.gemm_blockscale_fp32acc / gemm_per_tensor_fp32acc);
-fp32 outputs are also checked against the reference's own gemm_ref semantics
+fp32 accumulation with the FP8 MFMA's own 128-K step sum, in the K slices the
+library reports for the call (oracle.gemm_blockscale_mfma /
+gemm_per_tensor_mfma with opus_gemm.k_slices); fp32 outputs are also checked
+against the reference's own gemm_ref semantics
 (per-product fp32 sum, opus_gemm/block_scale_gemm/..._host.cc:66-90) with the
 reference's absolute tolerance scaled to the output magnitude.
 """
@@ -13,7 +15,7 @@ import torch
 
 import oracle
 from gcnasm_amd import opus_gemm, ops
-from helpers import bf16_compare, f32_compare
+from helpers import assert_parity, bf16_compare, f32_compare, tile_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -34,6 +36,21 @@ def ds_operands(M, N, K, seed, group_n=128, batch=1):
             qb[b], s = oracle.quant_fp8_1x128(xb[b])
         sfb.append(s)
     return qa, qb, np.stack(sfa), np.stack(sfb)
+
+
+def expect_bs(qa, qb, sfa, sfb, group_n, M_full=None, batch=1):
+    """fp32 result of the kernel the library picks for [M_full, N, K] (rows of
+    qa may be a subset of those)."""
+    M = qa.shape[0] if M_full is None else M_full
+    N, K = qb.shape
+    gps = opus_gemm.k_slices(M, N, K, batch)
+    return oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n, gps)
+
+
+def expect_pt(qa, qb, sa, sb, M_full=None):
+    M = qa.shape[0] if M_full is None else M_full
+    N, K = qb.shape
+    return oracle.gemm_per_tensor_mfma(qa, qb, sa, sb, opus_gemm.k_slices(M, N, K))
 
 
 def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
@@ -63,14 +80,12 @@ def run_bs(dev, qa, qb, sfa, sfb, out_dtype, group_n):
 def test_blockscale(dev, group_n, shape):
     M, N, K = shape
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + N, group_n=group_n)
-    want = oracle.gemm_blockscale_fp32acc(qa[0], qb[0], sfa[0], sfb[0], group_n)
+    want = expect_bs(qa[0], qb[0], sfa[0], sfb[0], group_n)
     C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, group_n)
     got = C[0].cpu().numpy()
     absdot = oracle.blockscale_absdot(qa[0], qb[0], sfa[0], sfb[0], group_n)
     ok, st = f32_compare(got, want, absdot=absdot)
-    print("bs f32 %s g%d: exact=%.5f max_ulp=%d bounded=%d bad=%d" % (
-        shape, group_n, st["exact"], st["max_ulp"], st["bounded"], st["bad"]), flush=True)
-    assert st["bad"] == 0
+    assert_parity(st, "bs f32 %s g%d" % (shape, group_n))
     # reference gemm_ref semantics (per-product fp32 sums): the reference's own
     # check is |diff| <= 1e-3 on its U[0,1) x U[-.5,.5) data; on N(0,1) data the
     # same check scaled to the output magnitude
@@ -79,32 +94,29 @@ def test_blockscale(dev, group_n, shape):
     Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, group_n)
     gb = Cb[0].view(torch.int16).cpu().numpy().view(np.uint16)
     ok, st = bf16_compare(gb, oracle.to_bf16_bits(want), absdot)
-    assert st["bad"] == 0
+    assert_parity(st, "bs bf16 %s g%d" % (shape, group_n))
 
 
 @pytest.mark.parametrize("shape", [(4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)])
 def test_blockscale_deepseek_configs(dev, shape):
     """The DeepSeek shapes the benchmark configuration names, run whole on the
-    GPU (fp32 and bf16 C) and checked on 40 rows: the first and last 8 and 24
-    spread between (the CPU oracle on every row would take minutes)."""
+    GPU (fp32 and bf16 C) and checked on the first and last 8 rows and one row
+    of every 256-row tile (the CPU oracle on every row would take minutes)."""
     M, N, K = shape
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=17)
-    rows = np.unique(np.concatenate([np.arange(8), np.arange(M - 8, M),
-                                     np.linspace(8, M - 9, 24).astype(np.int64)]))
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(M - 8, M), tile_rows(M)]))
     qa_r = np.ascontiguousarray(qa[0][rows])
     sfa_r = np.ascontiguousarray(sfa[0][:, rows])
-    want = oracle.gemm_blockscale_fp32acc(qa_r, qb[0], sfa_r, sfb[0], 128)
+    want = expect_bs(qa_r, qb[0], sfa_r, sfb[0], 128, M_full=M)
     absdot = oracle.blockscale_absdot(qa_r, qb[0], sfa_r, sfb[0], 128)
     C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
     ok, st = f32_compare(C[0].cpu().numpy()[rows], want, absdot=absdot)
-    print("bs f32 %s: exact=%.5f max_ulp=%d bounded=%d bad=%d" % (
-        shape, st["exact"], st["max_ulp"], st["bounded"], st["bad"]), flush=True)
-    assert st["bad"] == 0
+    assert_parity(st, "bs f32 %s" % (shape,))
     del C
     Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, 128)
     gb = Cb[0].view(torch.int16).cpu().numpy().view(np.uint16)[rows]
     ok, st = bf16_compare(gb, oracle.to_bf16_bits(want), absdot)
-    assert st["bad"] == 0
+    assert_parity(st, "bs bf16 %s" % (shape,))
 
 
 def test_blockscale_batched(dev):
@@ -112,10 +124,10 @@ def test_blockscale_batched(dev):
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=5, batch=batch)
     C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
     for b in range(batch):
-        want = oracle.gemm_blockscale_fp32acc(qa[b], qb[b], sfa[b], sfb[b], 128)
+        want = expect_bs(qa[b], qb[b], sfa[b], sfb[b], 128, batch=batch)
         absdot = oracle.blockscale_absdot(qa[b], qb[b], sfa[b], sfb[b], 128)
         ok, st = f32_compare(C[b].cpu().numpy(), want, absdot=absdot)
-        assert st["bad"] == 0, b
+        assert_parity(st, "batch %d" % b)
 
 
 def test_blockscale_batched_small_m(dev):
@@ -123,10 +135,10 @@ def test_blockscale_batched_small_m(dev):
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=9, batch=batch)
     C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
     for b in range(batch):
-        want = oracle.gemm_blockscale_fp32acc(qa[b], qb[b], sfa[b], sfb[b], 128)
+        want = expect_bs(qa[b], qb[b], sfa[b], sfb[b], 128, batch=batch)
         absdot = oracle.blockscale_absdot(qa[b], qb[b], sfa[b], sfb[b], 128)
         ok, st = f32_compare(C[b].cpu().numpy(), want, absdot=absdot)
-        assert st["bad"] == 0, b
+        assert_parity(st, "batch %d" % b)
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 512), (200, 1040, 1024), (1, 512, 256),
@@ -138,7 +150,7 @@ def test_per_tensor(dev, shape):
     xb = oracle.randn(N * K, 12).reshape(N, K)
     qa, sa = oracle.quant_fp8_per_tensor(xa)
     qb, sb = oracle.quant_fp8_per_tensor(xb)
-    want = oracle.gemm_per_tensor_fp32acc(qa, qb, sa[0], sb[0])
+    want = expect_pt(qa, qb, sa[0], sb[0])
     absdot = oracle.fp8_absdot(qa, qb) * float(sa[0]) * float(sb[0])
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     for dt in (torch.float32, torch.bfloat16):
@@ -150,7 +162,7 @@ def test_per_tensor(dev, shape):
         else:
             ok, st = bf16_compare(C.view(torch.int16).cpu().numpy().view(np.uint16),
                                   oracle.to_bf16_bits(want), absdot)
-        assert st["bad"] == 0, dt
+        assert_parity(st, "per-tensor %s %s" % (shape, dt))
 
 
 def test_per_tensor_from_float_on_gpu(dev):
@@ -165,10 +177,10 @@ def test_per_tensor_from_float_on_gpu(dev):
     torch.cuda.synchronize()
     oa, osa = oracle.quant_fp8_per_tensor(xa)
     ob, osb = oracle.quant_fp8_per_tensor(xb)
-    want = oracle.gemm_per_tensor_fp32acc(oa, ob, osa[0], osb[0])
+    want = expect_pt(oa, ob, osa[0], osb[0])
     absdot = oracle.fp8_absdot(oa, ob) * float(osa[0]) * float(osb[0])
     ok, st = f32_compare(C.cpu().numpy(), want, absdot=absdot)
-    assert st["bad"] == 0
+    assert_parity(st, "per-tensor from float")
 
 
 def test_splitk_reduce(dev):

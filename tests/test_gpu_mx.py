@@ -3,11 +3,10 @@
 Cases follow the reference's regression sweep (asm_f4gemm/run_tests.sh:37-57):
 a heuristic shape sweep, every manifest kernel at M=300 N=2048 K=1024, and
 split-K with log2 splits 1..4; plus config 1 of the benchmark, decode shapes,
-alpha/beta and error paths. Expected values come from
-oracle.gemm_mxfp8_fp32acc (exact 128-K step sums accumulated in fp32 in the
-kernel's K order, slices summed in order) rounded to bf16; the tolerance is
-the north-star rule in helpers.bf16_compare, with the MFMA truncation bound
-(helpers.MFMA_BOUND_FACTOR) for outputs that cancel.
+alpha/beta and error paths. Expected values come from oracle.gemm_mx_mfma
+(the FP8 MFMA's own 128-K step sum, accumulated in fp32 in the kernel's K
+order, slices summed in order) rounded to bf16; the tolerance is the
+north-star rule (helpers.bf16_compare / assert_parity).
 """
 import ctypes
 import re
@@ -19,7 +18,7 @@ import torch
 import oracle
 from gcnasm_amd import _lib, f4gemm
 from gcnasm_amd._lib import GaError
-from helpers import bf16_compare, mx_operands
+from helpers import assert_parity, bf16_compare, mx_operands
 
 pytestmark = pytest.mark.gpu
 
@@ -53,14 +52,12 @@ def run_mx(dev, qa, sa, qb, sb, cfg, log2_k_split=0, alpha=1.0, beta=0.0, c_in=N
 
 
 def expect(qa, sa, qb, sb, log2_k_split=0, alpha=1.0):
-    return oracle.to_bf16_bits(oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, log2_k_split, alpha))
+    return oracle.to_bf16_bits(oracle.gemm_mx_mfma(qa, sa, qb, sb, log2_k_split, alpha))
 
 
 def check(got, want, label, absdot):
     ok, st = bf16_compare(got, want, absdot)
-    print("%s: exact=%.5f max_ulp=%d bounded=%d bad=%d/%d" % (
-        label, st["exact"], st["max_ulp"], st["bounded"], st["bad"], st["n"]), flush=True)
-    assert st["bad"] == 0, "%s: %d outputs outside tolerance" % (label, st["bad"])
+    assert_parity(st, label)
     return st
 
 
@@ -93,8 +90,9 @@ def test_config1_heuristic(dev):
     got, _ = run_mx(dev, qa, sa, qb, sb, cfg, l2)
     st = check(got, expect(qa, sa, qb, sb, l2), "config1 " + cfg.knl_name,
                oracle.mx_absdot(qa, sa, qb, sb))
-    # all but the MFMA-truncation residue is bit-identical to the oracle
-    assert st["exact"] > 0.98
+    # bf16 outputs bit-identical to the MFMA-model oracle but for rounding
+    # boundaries the model's residual crosses
+    assert st["exact"] > 0.999
 
 
 @pytest.mark.parametrize("shape", [(128, 1024, 1024), (256, 2048, 2048), (300, 2048, 1024),
@@ -170,7 +168,7 @@ def test_alpha_beta(dev):
     c = oracle.to_bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
     cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_128x128")
     got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0, alpha=0.5, beta=2.0, c_in=c)
-    acc = oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, 0, 1.0)
+    acc = oracle.gemm_mx_mfma(qa, sa, qb, sb, 0, 1.0)
     v = (np.float32(0.5) * acc).astype(np.float32)
     v = (v + (np.float32(2.0) * oracle.bf16_bits_to_f32(c)).astype(np.float32)).astype(np.float32)
     check(got, oracle.to_bf16_bits(v), "alpha/beta", 0.5 * oracle.mx_absdot(qa, sa, qb, sb))
@@ -272,8 +270,123 @@ def test_decode_path_plain_b_and_epilogue(dev, M):
     rng = np.random.default_rng(M)
     c_in = oracle.to_bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
     got, _ = run_mx(dev, qa, sa, qb, sb, cfg, 0, alpha=0.5, beta=2.0, c_in=c_in)
-    acc = oracle.gemm_mxfp8_fp32acc(qa, sa, qb, sb, 0, 1.0)
+    acc = oracle.gemm_mx_mfma(qa, sa, qb, sb, 0, 1.0)
     want_f = (np.float32(0.5) * acc).astype(np.float32) + np.float32(2.0) * \
         oracle.bf16_bits_to_f32(c_in)
     check(got, oracle.to_bf16_bits(want_f.astype(np.float32)), "decode plain-B alpha/beta M=%d" % M,
           0.5 * oracle.mx_absdot(qa, sa, qb, sb))
+
+
+@pytest.mark.parametrize("name", PP_KERNELS)
+def test_persistent_many_tiles(dev, name):
+    """More 256x256 tiles (17 x 16 = 272) than the persistent grid has
+    workgroups (one per CU, 256 on MI355X), so workgroups compute a second
+    tile after the first (LDS reuse, staged epilogue, split-K partials of a
+    later tile); every output checked."""
+    M, N, K = 4352, 4096, 256
+    cfg = cfg_named(name)
+    l2 = 1 if cfg.splitK else 0
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=4352)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    check(got, expect(qa, sa, qb, sb, l2), "persistent %s gdz=%d" % (name, ld.gdz),
+          oracle.mx_absdot(qa, sa, qb, sb))
+
+
+@pytest.mark.parametrize("MNKL", [(64, 8192, 28672, 1), (64, 8192, 32768, 2),
+                                  (24, 8192, 16384, 1)])
+def test_decode_deep_k_split(dev, MNKL):
+    """The decode kernel's four-steps-in-flight variant with K split across
+    the waves of a workgroup (2 or 4 slices of at least 64 steps each), for
+    the 33-64-row and 17-32-row instantiations."""
+    M, N, K, l2 = MNKL
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_256x128_splitK")
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=M + l2, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    assert ld.gdz == 1 << l2
+    check(got, expect(qa, sa, qb, sb, l2), "decode deep M=%d N=%d K=%d gdz=%d" %
+          (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
+def _mx_device_problem(dev, M, N, K, cfg, l2, seed):
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=seed)
+    sh = f4gemm.Shape(M, N, K)
+    a_pad = np.zeros((sh.a_rows_pad(), K), dtype=np.uint8)
+    a_pad[:M] = qa
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    A, B = t(a_pad), t(f4gemm.shuffle_weight_16x16(qb, N, K))
+    SA = t(f4gemm.shuffle_scale(sa, M, K // 32, sh.scale_a_rows(), sh.scale_cols()))
+    SB = t(f4gemm.shuffle_scale(sb, N, K // 32, sh.scale_b_rows(), sh.scale_cols()))
+    D = torch.full((sh.d_rows_pad(), N), float("nan"), dtype=torch.bfloat16, device=dev)
+    ld = f4gemm.make_launch(cfg, M, N, K, l2)
+    args = f4gemm.fill_args(D, None, A, B, SA, SB, M, N, K, N, sh.scale_cols(), sh.scale_cols(),
+                            1.0, 0.0, ld.log2_k_split)
+    keep = (A, B, SA, SB)
+    return (qa, sa, qb, sb), D, ld, args, keep
+
+
+@pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_128x128_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_64x256_splitK"])
+def test_ws_handle_graph_replay_survives_grow(dev, name):
+    """ga_kernel_launch_ws_handle: a split-K GEMM captured into a HIP graph
+    with its workspace found through a device slot keeps giving the eager
+    result after the slot's buffer is grown (and moved) between replays; a
+    slot never reserved is refused on the host."""
+    from gcnasm_amd import flatmm_splitk as fs
+    M, N, K, l2 = 256, 1024, 4096, 2
+    cfg = cfg_named(name)
+    (qa, sa, qb, sb), D, ld, args, keep = _mx_device_problem(dev, M, N, K, cfg, l2, 21)
+    assert ld.gdz == 4
+    kern = f4gemm.Kernel().load(None, cfg)
+    need = kern.workspace_bytes(ld, M, N)
+    h = fs.WorkspaceHandle()
+    try:
+        with pytest.raises(GaError) as e:
+            kern.launch(args, ld.gdx, ld.gdy, ld.gdz, ws_handle=h)
+        assert e.value.status == _lib.GA_ERR_WORKSPACE
+        h.reserve(need)
+        kern.launch(args, ld.gdx, ld.gdy, ld.gdz, ws_handle=h)
+        torch.cuda.synchronize()
+        eager = D[:M].view(torch.int16).cpu().numpy().view(np.uint16).copy()
+        check(eager, expect(qa, sa, qb, sb, l2), "ws handle eager %s" % name,
+              oracle.mx_absdot(qa, sa, qb, sb))
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            kern.launch(args, ld.gdx, ld.gdy, ld.gdz, stream=s, ws_handle=h)
+        ptr0 = h.query()[0]
+        for rep in range(6):
+            if rep == 3:
+                h.reserve(3 * need)  # grows and moves the workspace
+                assert h.query()[0] != ptr0
+            D.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+            np.testing.assert_array_equal(got, eager, err_msg="replay %d" % rep)
+            kern.launch(args, ld.gdx, ld.gdy, ld.gdz, ws_handle=h)  # eager work between
+            torch.cuda.synchronize()
+        del g
+    finally:
+        h.close()
+    del keep
+
+
+def test_library_workspace_refused_under_capture(dev):
+    """A split-K launch with no caller workspace uses the library's own buffer,
+    which a later call may reallocate: refused while the stream captures."""
+    M, N, K, l2 = 256, 1024, 4096, 2
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_256x256_splitK")
+    _, D, ld, args, keep = _mx_device_problem(dev, M, N, K, cfg, l2, 22)
+    kern = f4gemm.Kernel().load(None, cfg)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(GaError) as e:
+        with torch.cuda.graph(g, stream=s):
+            kern.launch(args, ld.gdx, ld.gdy, ld.gdz, stream=s)
+    assert e.value.status == _lib.GA_ERR_WORKSPACE
+    torch.cuda.synchronize()
+    del g, keep
