@@ -12,8 +12,9 @@ quantised on the GPU by the library's MX quantiser (scale rule floor(log2(amax/4
 Also measured (reported in "decode" and "decode_other"): the decode GEMMs
 M=16, N=28672, K=8192 and M=16, N=8192, K=28672, then the same at M=1 and
 M=64 (the configuration's M in {1, 16, 64}), with weights from N(0, 0.02),
-rotating 3 weight sets (> 256 MB Infinity Cache), at the reference driver's
-default log2_k_split=0.
+rotating 3 weight sets (> 256 MB Infinity Cache), at the heuristic's split
+(log2_k_split = -1; the configuration allows split-K) and, beside it, at the
+reference driver's default log2_k_split = 0.
 
 "mxfp4" / "mxfp4_decode" run the same two workloads with OCP e2m1 operands.
 The reference's own f4gemm kernels are MXFP4; its published table
@@ -61,11 +62,17 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 512 MiB device-to-device twice (counter calibration "
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
+    ap.add_argument("--legs", default="all",
+                    help="comma-separated subset of: " + ",".join(LEGS) + " (default all; "
+                         "one leg at a time attributes rocprofv3 counters to one workload)")
     return ap.parse_args()
+
+
+LEGS = ("decode", "mxfp8_8192", "mxfp8_4096", "mxfp4_decode", "quant", "blockscale",
+        "deepseek", "mxfp4", "a16w16", "cpu")
 
 
 def mx_inputs(torch, M, N, K, b_std=1.0, nsets=1, seed=0):
@@ -385,79 +392,219 @@ def scaled_inputs(torch, M, N, K, seed=2):
     return xa, xb
 
 
+def time_opus(torch, opus_gemm, a, b, sfa, sfb, c, group_n, steps, warmup):
+    """Average launch duration (us) of one fp32-scale GEMM, kargs built once
+    (per-tensor when group_n is 0)."""
+    m, k = a.shape
+    n = b.shape[0]
+    ka = opus_gemm.make_kargs(a, b, c, sfa, sfb, m, n, k, 1, group_n)
+    out = opus_gemm._out_dtype(c)
+    if group_n == 0:
+        fn = lambda: opus_gemm.fp8_gemm(ka, out)  # noqa: E731
+    else:
+        fn = lambda: opus_gemm.gemm_a8w8_blockscale(ka, out, group_n)  # noqa: E731
+    return time_call(torch, fn, steps, warmup)
+
+
+def opus_leg(workload, M, N, K, us, extra=None):
+    flops = 2.0 * M * N * K
+    tf = flops / us / 1e6
+    d = {"workload": workload, "value": round(tf, 1), "unit": "TFLOP/s",
+         "kernel_avg_us": round(us, 2),
+         "roofline": roofline(workload, tf, "mfma", FP8_PEAK_TFLOPS, "TFLOP/s")}
+    d.update(extra or {})
+    return d
+
+
 def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
-    """DeepSeek block-scale (fp32 C) and per-tensor (bf16 C) GEMMs at 8192^3."""
+    """DeepSeek block-scale (fp32 C) and per-tensor (bf16 C) GEMMs at 8192^3
+    on N(0,1) inputs quantised on the GPU, and the block-scale GEMM on the
+    reference driver's own operand distribution (gemm_a8w8_blockscale_host.cc:
+    207-210: A ~ U[0,1), B ~ U[-0.5,0.5) converted to E4M3, SFA and SFB ~
+    U[0.8,1.2)) for a like-for-like comparison with its published number (this
+    power-limited part's clock depends on the operand bits)."""
     n = 8192
     xa, xb = scaled_inputs(torch, n, n, n)
     qa, sfa = ops.quant_fp8_1x128(xa)
     qb, sfb = ops.quant_fp8_128x128(xb)
     c = torch.empty((n, n), dtype=torch.float32, device="cuda:0")
-    us = time_call(torch, lambda: opus_gemm.blockscale_gemm(qa, qb, sfa, sfb, c), steps, warmup)
-    del qa, qb, sfa, sfb, c
-    flops = 2.0 * n ** 3
-    bs = {"workload": "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out",
-          "value": round(flops / us / 1e6, 1), "unit": "TFLOP/s", "kernel_avg_us": round(us, 2),
-          "frac_fp8_peak": round(flops / us / 1e6 / FP8_PEAK_TFLOPS, 4),
-          "reference_published": REF_BLOCKSCALE_8192_TFLOPS,
-          "vs_reference": round(flops / us / 1e6 / REF_BLOCKSCALE_8192_TFLOPS, 4)}
+    us = time_opus(torch, opus_gemm, qa, qb, sfa, sfb, c, 128, steps, warmup)
+    del qa, qb, sfa, sfb
+    bs = opus_leg("fp8_blockscale_1x128_128x128_8192x8192x8192_f32out", n, n, n, us,
+                  {"data": "N(0,1), quantised on the GPU (1x128 / 128x128 amax/448)"})
+    bs["frac_fp8_peak"] = bs["roofline"]["frac"]
+    bs["reference_published"] = REF_BLOCKSCALE_8192_TFLOPS
+    bs["vs_reference"] = round(bs["value"] / REF_BLOCKSCALE_8192_TFLOPS, 4)
     qa, sa = ops.quant_fp8_per_tensor(xa)
     qb, sb = ops.quant_fp8_per_tensor(xb)
-    c = torch.empty((n, n), dtype=torch.bfloat16, device="cuda:0")
-    us = time_call(torch, lambda: opus_gemm.per_tensor_gemm(qa, qb, sa, sb, c), steps, warmup)
-    pt = {"workload": "fp8_per_tensor_8192x8192x8192_bf16out",
-          "value": round(flops / us / 1e6, 1), "unit": "TFLOP/s", "kernel_avg_us": round(us, 2),
-          "frac_fp8_peak": round(flops / us / 1e6 / FP8_PEAK_TFLOPS, 4)}
-    del xa, xb, qa, qb, c
+    cb = torch.empty((n, n), dtype=torch.bfloat16, device="cuda:0")
+    us = time_opus(torch, opus_gemm, qa, qb, sa, sb, cb, 0, steps, warmup)
+    pt = opus_leg("fp8_per_tensor_8192x8192x8192_bf16out", n, n, n, us)
+    pt["frac_fp8_peak"] = pt["roofline"]["frac"]
+    del xa, xb, qa, qb, cb
+    # the reference driver's distribution
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(7)
+    ra = torch.rand((n, n), device="cuda:0", generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    rb = (torch.rand((n, n), device="cuda:0", generator=g) - 0.5).to(
+        torch.float8_e4m3fn).view(torch.uint8)
+    rsfa = torch.rand((n // 128, n), device="cuda:0", generator=g) * 0.4 + 0.8
+    rsfb = torch.rand((n // 128, n // 128), device="cuda:0", generator=g) * 0.4 + 0.8
+    us = time_opus(torch, opus_gemm, ra, rb, rsfa, rsfb, c, 128, steps, warmup)
+    bsr = opus_leg("fp8_blockscale_1x128_128x128_8192x8192x8192_f32out_refdata", n, n, n, us,
+                   {"data": "the reference driver's: A~U[0,1) B~U[-.5,.5) as E4M3, "
+                            "SFA/SFB~U[0.8,1.2) (gemm_a8w8_blockscale_host.cc:207-210)",
+                    "reference_published": REF_BLOCKSCALE_8192_TFLOPS})
+    bsr["vs_reference"] = round(bsr["value"] / REF_BLOCKSCALE_8192_TFLOPS, 4)
+    bs["refdata"] = bsr
+    del ra, rb, rsfa, rsfb, c
     torch.cuda.empty_cache()
     return bs, pt
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of the 8192^3 kernel from the committed rocprofv3
-    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a 512 MiB copy),
-    or None when no summary for this kernel is committed."""
-    path = os.path.join(ROOT, "profiles", "mxfp8_8192_traffic.json")
+DEEPSEEK_SHAPES = ((4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536))
+
+
+def deepseek_legs(torch, ops, opus_gemm, steps, warmup):
+    """The DeepSeek-style block-scale configurations (1x128 activation /
+    128x128 weight fp32 scales) on N(0,1) inputs quantised on the GPU, fp32 C
+    (the reference's) and bf16 C (the north star's)."""
+    out = []
+    for M, N, K in DEEPSEEK_SHAPES:
+        xa, xb = scaled_inputs(torch, M, N, K, seed=17)
+        qa, sfa = ops.quant_fp8_1x128(xa)
+        qb, sfb = ops.quant_fp8_128x128(xb)
+        del xa, xb
+        c32 = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+        c16 = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0")
+        us32 = time_opus(torch, opus_gemm, qa, qb, sfa, sfb, c32, 128, steps, warmup)
+        us16 = time_opus(torch, opus_gemm, qa, qb, sfa, sfb, c16, 128, steps, warmup)
+        wl = "fp8_blockscale_deepseek_%dx%dx%d" % (M, N, K)
+        d = opus_leg(wl + "_f32out", M, N, K, us32)
+        d["bf16out"] = opus_leg(wl + "_bf16out", M, N, K, us16)
+        out.append(d)
+        del qa, qb, sfa, sfb, c32, c16
+        torch.cuda.empty_cache()
+    return out
+
+
+def measured_traffic(workload, kernel=None):
+    """HBM bytes per launch of a workload's kernel from the committed
+    rocprofv3 counter summary (profiles/traffic.json: FETCH_SIZE +
+    WRITE_SIZE per dispatch, each calibrated on a 512 MiB device copy), or
+    None when none is committed for it (or it was measured on another kernel)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            t = json.load(f)
-    except (OSError, ValueError):
+            t = json.load(f)["workloads"][workload]
+    except (OSError, ValueError, KeyError):
         return None
-    if t.get("kernel") != kernel:
+    if kernel is not None and t.get("kernel") not in (None, kernel):
         return None
     return t.get("bytes_per_launch")
 
 
-def cpu_baseline(M, N, K, seconds):
-    """Reference CPU GEMM on a bounded row sample of the M x N x K problem."""
+def roofline(workload, achieved, bound, peak, unit, kernel=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, kernel)}
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def _mx_cpu_operands(np, oracle, rows, K, seed, std=1.0):
+    """Dequantised fp32 MX operand (what reference_gemm takes) for rows x K."""
+    x = oracle.gen_mx_input(rows, K, seed, std, 4)
+    q, sc = oracle.quant_mxfp8(x)
+    return np.ascontiguousarray(oracle.mx_dequant(q, sc).astype(np.float32))
+
+
+def cpu_legs():
+    """The CPU baselines of the benchmark configurations, timed on this host:
+    the reference's own reference_gemm (asm_f4gemm/f4gemm_ref.hpp:181-222,
+    compiled in place into oracle/_ref; f64 accumulation over dequantised
+    fp32 operands, its own thread pool) for the MX and per-tensor GEMMs, and
+    the oracle's port of the block-scale gemm_ref (gemm_a8w8_blockscale_host.cc:
+    66-90: per-product fp32 sum, OpenMP) whose source does not build here.
+    Full runs except 8192^3, timed on a 256-row slice and extrapolated."""
     import numpy as np
     import oracle
     R = oracle.load_ref()
+    O = oracle.load()
     kind = "reference" if R is not None else "port"
-    rng = np.random.default_rng(0)
-    B = rng.standard_normal((N, K), dtype=np.float32)
+    threads = R.ref_threads(1 << 30) if R is not None else (os.cpu_count() or 1)
+    omp = int(os.environ.get("OMP_NUM_THREADS") or (os.cpu_count() or 1))
 
-    def run(rows):
-        A = rng.standard_normal((rows, K), dtype=np.float32)
-        D = np.empty((rows, N), dtype=np.float32)
+    def ref_gemm(A, B):
+        M, K = A.shape
+        N = B.shape[0]
+        D = np.empty((M, N), dtype=np.float32)
         t0 = time.perf_counter()
         if R is not None:
-            R.ref_reference_gemm(oracle.p(A), oracle.p(B), rows, N, K, 1.0, oracle.p(D))
+            R.ref_reference_gemm(oracle.p(A), oracle.p(B), M, N, K, 1.0, oracle.p(D))
         else:
-            oracle.load().or_reference_gemm(oracle.p(A), oracle.p(B), rows, N, K, 1.0,
-                                            oracle.p(D))
+            O.or_reference_gemm(oracle.p(A), oracle.p(B), M, N, K, 1.0, oracle.p(D))
         return time.perf_counter() - t0
 
-    threads = R.ref_threads(1 << 30) if R is not None else (os.cpu_count() or 1)
-    probe_rows = max(threads, 8)
-    t = run(probe_rows)
-    rows = int(min(M, max(probe_rows, probe_rows * seconds / max(t, 1e-3))))
-    rows = max(threads, rows // threads * threads)
-    t = run(rows)
-    flops = 2.0 * rows * N * K
-    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": min(threads, rows),
-            "kind": kind,
-            "sample": "reference_gemm (f64 accumulate over dequantised fp32 operands) on %d of "
-                      "%d rows of the %dx%dx%d GEMM, %.1f s" % (rows, M, M, N, K, t)}
+    out = []
+
+    def add(workload, M, N, K, t, kind_, cores, impl, rows=None):
+        flops = 2.0 * (rows or M) * N * K
+        e = {"workload": workload, "value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+             "seconds": round(t, 3), "cores": cores, "kind": kind_, "impl": impl}
+        if rows:
+            e["sample"] = "%d of %d rows, extrapolated: %.1f s for the whole GEMM" % (
+                rows, M, t * M / rows)
+        out.append(e)
+        return e
+
+    # MX / per-tensor: reference_gemm over dequantised operands
+    for (M, N, K), wl, std_b in (((256, 256, 512), "mxfp8_gemm_256x256x512", 1.0),
+                                 ((4096, 4096, 4096), "mxfp8_gemm_4096x4096x4096", 1.0),
+                                 ((16, 28672, 8192), "mxfp8_gemm_decode_16x28672x8192", 0.02),
+                                 ((16, 8192, 28672), "mxfp8_gemm_decode_16x8192x28672", 0.02)):
+        A = _mx_cpu_operands(np, oracle, M, K, 11, 1.0)
+        B = _mx_cpu_operands(np, oracle, N, K, 12, std_b)
+        add(wl, M, N, K, ref_gemm(A, B), kind, min(threads, M), "reference_gemm")
+        del A, B
+    rng = np.random.default_rng(0)
+    n = 4096
+    xa, xb = rng.standard_normal((n, n), dtype=np.float32), rng.standard_normal((n, n), dtype=np.float32)
+    qa, sa = oracle.quant_fp8_per_tensor(xa)
+    qb, sb = oracle.quant_fp8_per_tensor(xb)
+    tab = oracle.e4m3_decode_table()
+    A = np.ascontiguousarray(tab[qa] * sa[0])
+    B = np.ascontiguousarray(tab[qb] * sb[0])
+    add("fp8_per_tensor_4096x4096x4096", n, n, n, ref_gemm(A, B), kind, threads, "reference_gemm")
+    del xa, xb, qa, qb, A, B
+    # block scale: the gemm_ref port
+    for M, N, K in DEEPSEEK_SHAPES:
+        qa, sfa = oracle.quant_fp8_1x128(rng.standard_normal((M, K), dtype=np.float32))
+        qb, sfb = oracle.quant_fp8_128x128(rng.standard_normal((N, K), dtype=np.float32))
+        t0 = time.perf_counter()
+        oracle.gemm_blockscale_ref(qa, qb, sfa, sfb, 128)
+        add("fp8_blockscale_deepseek_%dx%dx%d" % (M, N, K), M, N, K, time.perf_counter() - t0,
+            "port", omp, "gemm_ref port (oracle.c or_gemm_blockscale_ref)")
+        del qa, qb
+    # the headline: 8192^3 on a 256-row slice
+    n, rows = 8192, 256
+    A = _mx_cpu_operands(np, oracle, rows, n, 11, 1.0)
+    B = _mx_cpu_operands(np, oracle, n, n, 12, 1.0)
+    head = add("mxfp8_gemm_8192x8192x8192", n, n, n, ref_gemm(A, B), kind, min(threads, rows),
+               "reference_gemm", rows=rows)
+    del A, B
+    return head, out
 
 
 def main():
@@ -466,6 +613,13 @@ def main():
         print("bench.py: this build runs on one GPU only (--gpus %d requested); the sharded "
               "design is described in DESIGN.md" % args.gpus, file=sys.stderr)
         sys.exit(2)
+    legs = set(LEGS) if args.legs == "all" else set(args.legs.split(","))
+    unknown = legs - set(LEGS)
+    if unknown:
+        print("bench.py: unknown legs %s" % sorted(unknown), file=sys.stderr)
+        sys.exit(2)
+    if args.no_cpu:
+        legs.discard("cpu")
     import torch
     from gcnasm_amd import f4gemm, opus_gemm, ops
 
@@ -477,77 +631,116 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    # decode, M=16: HBM-bound; rotate weight sets so the Infinity Cache cannot
+    extra = {}
+    # decode: HBM-bound; rotate weight sets so the Infinity Cache cannot
     # serve them; log2_k_split=0 is the reference driver's default. Measured
     # first, on an idle GPU: right after the MFMA-heavy legs the power
     # controller leaves the memory path a few percent slower for about a second.
-    decode = []
-    for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672), (1, 28672, 8192),
-                       (1, 8192, 28672), (64, 28672, 8192), (64, 8192, 28672)):
-        da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=1)
-        dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30), args.warmup,
-                       log2_k_split=0)
-        dbytes = dM * dK + dN * dK + (dM + dN) * dK / 32 + 2 * dM * dN
-        dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
-        decode.append({"workload": "mxfp8_gemm_decode_%dx%dx%d" % (dM, dN, dK),
-                       "value": round(dgbs, 1), "unit": "GB/s", "kernel": dr["cfg"].knl_name,
-                       "grid": [dr["ld"].gdx, dr["ld"].gdy, dr["ld"].gdz],
-                       "kernel_avg_us": round(dr["avg_us"], 2),
-                       "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4),
-                       "algorithmic_bytes": int(dbytes), "weight_sets": 3})
-        del da, dbs
-        torch.cuda.empty_cache()
+    if "decode" in legs:
+        # each shape at the heuristic's own split (log2_k_split = -1: the
+        # configuration allows split-K; this is the reported value) and at the
+        # reference driver's default log2_k_split = 0
+        decode = []
+        for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672), (1, 28672, 8192),
+                           (1, 8192, 28672), (64, 28672, 8192), (64, 8192, 28672)):
+            da, dbs = mx_problem(torch, ops, f4gemm, dM, dN, dK, b_std=0.02, nsets=3, seed=1)
+            dbytes = dM * dK + dN * dK + (dM + dN) * dK / 32 + 2 * dM * dN
+            wl = "mxfp8_gemm_decode_%dx%dx%d" % (dM, dN, dK)
+            res = {}
+            for l2 in (-1, 0):
+                dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30),
+                               args.warmup, log2_k_split=l2)
+                dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
+                res[l2] = {"value": round(dgbs, 1), "unit": "GB/s", "kernel": dr["cfg"].knl_name,
+                           "log2_k_split": dr["ld"].log2_k_split,
+                           "grid": [dr["ld"].gdx, dr["ld"].gdy, dr["ld"].gdz],
+                           "kernel_avg_us": round(dr["avg_us"], 2),
+                           "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4)}
+            e = {"workload": wl}
+            e.update(res[-1])
+            e.update({"algorithmic_bytes": int(dbytes), "weight_sets": 3,
+                      "roofline": roofline(wl, res[-1]["value"], "hbm", HBM_PEAK_GBS, "GB/s"),
+                      "log2_k_split_0": res[0]})
+            decode.append(e)
+            del da, dbs
+            torch.cuda.empty_cache()
+        extra["decode"] = decode[0]
+        extra["decode_other"] = decode[1:]
 
     M = N = K = 8192
-    a, bs = mx_problem(torch, ops, f4gemm, M, N, K)
-    r = time_gemm(torch, f4gemm, a, bs, M, N, K, args.steps, args.warmup)
     flops = 2.0 * M * N * K
-    tflops_wall = flops * args.steps / r["wall_s"] / 1e12
-    achieved = flops / (r["avg_us"] * 1e-6) / 1e12
-    ceiling = mfma_ceiling(torch, a.codes)
-    del a, bs
-    torch.cuda.empty_cache()
-
-    time.sleep(1.0)
-    mxfp4_decode = mxfp4_decode_leg(torch, ops, f4gemm, 20, 5)
-    quant = quant_legs(torch, 20, 5)
-    blockscale, per_tensor = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
-    mxfp4 = mxfp4_leg(torch, ops, f4gemm, 20, 5)
-    a16w16 = a16w16_leg(torch, 50, 10)
+    r = None
+    if "mxfp8_8192" in legs:
+        a, bs = mx_problem(torch, ops, f4gemm, M, N, K)
+        r = time_gemm(torch, f4gemm, a, bs, M, N, K, args.steps, args.warmup)
+        extra["mfma_ceiling"] = mfma_ceiling(torch, a.codes)
+        del a, bs
+        torch.cuda.empty_cache()
+        time.sleep(1.0)
+    if "mxfp8_4096" in legs:
+        n4 = 4096
+        a, bs = mx_problem(torch, ops, f4gemm, n4, n4, n4)
+        r4 = time_gemm(torch, f4gemm, a, bs, n4, n4, n4, max(args.steps, 50), args.warmup)
+        tf4 = 2.0 * n4 ** 3 / (r4["avg_us"] * 1e-6) / 1e12
+        wl = "mxfp8_gemm_4096x4096x4096"
+        extra["mxfp8_4096"] = {"workload": wl, "value": round(tf4, 1), "unit": "TFLOP/s",
+                               "kernel": r4["cfg"].knl_name,
+                               "grid": [r4["ld"].gdx, r4["ld"].gdy, r4["ld"].gdz],
+                               "kernel_avg_us": round(r4["avg_us"], 2),
+                               "roofline": roofline(wl, tf4, "mfma", FP8_PEAK_TFLOPS, "TFLOP/s",
+                                                    r4["cfg"].knl_name)}
+        del a, bs
+        torch.cuda.empty_cache()
+    if "mxfp4_decode" in legs:
+        extra["mxfp4_decode"] = mxfp4_decode_leg(torch, ops, f4gemm, 20, 5)
+    if "quant" in legs:
+        extra["quantisers"] = quant_legs(torch, 20, 5)
+    if "blockscale" in legs:
+        extra["blockscale"], extra["per_tensor"] = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
+    if "deepseek" in legs:
+        extra["deepseek"] = deepseek_legs(torch, ops, opus_gemm, 30, 5)
+    if "mxfp4" in legs:
+        extra["mxfp4"] = mxfp4_leg(torch, ops, f4gemm, 20, 5)
+    if "a16w16" in legs:
+        extra["a16w16_splitk"] = a16w16_leg(torch, 50, 10)
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
-        "value": round(tflops_wall, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r["wall_s"] / args.steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3 x e8m0 (MX 1x32) -> fp32 acc -> bf16",
         "data": "synthetic: N(0,1)*2^U[-4,4] per 1x32 block, quantised on GPU",
-        "config": {"workload": "mxfp8_gemm_8192x8192x8192", "M": M, "N": N, "K": K,
-                   "kernel": r["cfg"].knl_name, "grid": [r["ld"].gdx, r["ld"].gdy, r["ld"].gdz],
-                   "pct_fp8_peak": round(100.0 * tflops_wall / FP8_PEAK_TFLOPS, 2),
-                   "kernel_best_us": round(r["best_us"], 2),
-                   "kernel_median_us": round(r["median_us"], 2)},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic(r["cfg"].knl_name)},
-        "decode": decode[0],
-        "decode_other": decode[1:],
-        "mfma_ceiling": ceiling,
-        "blockscale": blockscale,
-        "per_tensor": per_tensor,
-        "mxfp4": mxfp4,
-        "mxfp4_decode": mxfp4_decode,
-        "quantisers": quant,
-        "a16w16_splitk": a16w16,
     }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
+    if r is not None:
+        tflops_wall = flops * args.steps / r["wall_s"] / 1e12
+        achieved = flops / (r["avg_us"] * 1e-6) / 1e12
+        out.update({
+            "value": round(tflops_wall, 2),
+            "ms_per_step": round(r["wall_s"] / args.steps * 1e3, 4),
+            "config": {"workload": "mxfp8_gemm_8192x8192x8192", "M": M, "N": N, "K": K,
+                       "kernel": r["cfg"].knl_name,
+                       "grid": [r["ld"].gdx, r["ld"].gdy, r["ld"].gdz],
+                       "pct_fp8_peak": round(100.0 * tflops_wall / FP8_PEAK_TFLOPS, 2),
+                       "kernel_best_us": round(r["best_us"], 2),
+                       "kernel_median_us": round(r["median_us"], 2)},
+            "roofline": roofline("mxfp8_gemm_8192x8192x8192", achieved, "mfma", FP8_PEAK_TFLOPS,
+                                 "TFLOP/s", r["cfg"].knl_name),
+        })
+    else:
+        out.update({"value": None, "ms_per_step": None,
+                    "config": {"workload": "legs: " + ",".join(sorted(legs))}})
+    out.update(extra)
+    if "cpu" in legs:
+        head, per_config = cpu_legs()
+        out["cpu_baseline"] = {k: head[k] for k in ("value", "unit", "cores", "kind")}
+        out["cpu_baseline"]["sample"] = "%s on %s" % (head["impl"], head["sample"])
+        out["cpu_baselines"] = per_config
+        out["cpu_host"] = cpu_info()
     print(json.dumps(out), flush=True)
 
 

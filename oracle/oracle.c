@@ -569,22 +569,38 @@ void or_gemm_blockscale_ref(const uint8_t* A, const uint8_t* B, const float* sfa
                             const float* sfb, float* C, int M, int N, int K, int lda,
                             int ldb, int ldc, int stride_sfa, int stride_sfb, int group_n)
 {
-#pragma omp parallel for schedule(static)
+    /* Per output the same fp32 operations in the same order as the
+     * reference (decode, a*b, *scale, +=); a decode table and four output
+     * columns per pass (four independent add chains) only make it faster. */
+    float dec[256];
+    for (int c = 0; c < 256; c++)
+        dec[c] = or_e4m3_decode((uint8_t)c);
+#pragma omp parallel for schedule(dynamic, 1)
     for (int i = 0; i < M; i++)
-        for (int j = 0; j < N; j++) {
-            float sum = 0.0f;
+        for (int j0 = 0; j0 < N; j0 += 4) {
+            int nj = N - j0 < 4 ? N - j0 : 4;
+            float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint8_t* a = A + (size_t)i * lda;
             for (int g = 0; g < K / 128; g++) {
                 float sa = sfa[(size_t)g * stride_sfa + i];
-                float sb = sfb_at(sfb, g, j, stride_sfb, group_n);
-                float scale = sa * sb;
+                float scale[4];
+                const uint8_t* b[4];
+                for (int t = 0; t < 4; t++) {
+                    int j = j0 + (t < nj ? t : 0);
+                    scale[t] = sa * sfb_at(sfb, g, j, stride_sfb, group_n);
+                    b[t] = B + (size_t)j * ldb;
+                }
                 for (int p = g * 128; p < g * 128 + 128; p++) {
-                    float prod = or_e4m3_decode(A[(size_t)i * lda + p]) *
-                                 or_e4m3_decode(B[(size_t)j * ldb + p]);
-                    prod = prod * scale;
-                    sum = sum + prod;
+                    float av = dec[a[p]];
+                    for (int t = 0; t < 4; t++) {
+                        float prod = av * dec[b[t][p]];
+                        prod = prod * scale[t];
+                        sum[t] = sum[t] + prod;
+                    }
                 }
             }
-            C[(size_t)i * ldc + j] = sum;
+            for (int t = 0; t < nj; t++)
+                C[(size_t)i * ldc + j0 + t] = sum[t];
         }
 }
 

@@ -71,6 +71,31 @@ def test_opus_kargs_validation():
     assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 128, 0, None) == _lib.GA_ERR_ARG
     ka.k = ka.stride_a = ka.stride_b = 256
     assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 64, 0, None) == _lib.GA_ERR_ARG
+    # 256 rows of A (or B) beyond the 4 GiB a buffer descriptor addresses
+    ka.stride_a = 1 << 24
+    assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 128, 0, None) == _lib.GA_ERR_SHAPE
+    assert l.ga_fp8_gemm_per_tensor(ctypes.byref(ka), 0, None) == _lib.GA_ERR_SHAPE
+    ka.stride_a = 256
+    ka.stride_b = 1 << 24
+    assert l.ga_gemm_a8w8_blockscale(ctypes.byref(ka), 128, 0, None) == _lib.GA_ERR_SHAPE
+
+
+def test_mx_extent_beyond_4gib_is_rejected():
+    """512 rows of a row stride past 2^23 bytes, or a scale matrix past 4 GiB,
+    cannot be addressed from a tile's buffer descriptor: GA_ERR_SHAPE before
+    any device call."""
+    l = _lib.lib()
+    args = _lib.F4gemmKargs()
+    l.ga_fill_args(ctypes.byref(args), 0x1000, None, 0x1000, 0x1000, 0x1000, 0x1000,
+                   256, 256, 1024, 256, 32, 32, 1.0, 0.0, 0)
+    args.stride_A0 = 1 << 23
+    assert l.ga_kernel_launch(0, ctypes.byref(args), 1, 1, 1, None, 0, None) == _lib.GA_ERR_SHAPE
+    args.stride_A0 = 1024
+    args.stride_B0 = 1 << 23
+    idx = ctypes.c_int()
+    assert l.ga_kernel_find(b"ga_mxfp8_bf16_noBpreShuffle_256x256", ctypes.byref(idx)) == 0
+    assert l.ga_kernel_launch(idx.value, ctypes.byref(args), 1, 1, 1, None, 0, None) == \
+        _lib.GA_ERR_SHAPE
 
 
 def test_mx_launch_validation_without_gpu():
