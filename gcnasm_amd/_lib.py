@@ -199,6 +199,7 @@ SIGNATURES = {
     "ga_kernel_workspace_bytes": (_sz, [_i, ctypes.POINTER(LaunchDesc), _i, _i]),
     "ga_kernel_launch": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _sz, _vp]),
     "ga_kernel_launch_ws_handle": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _vp]),
+    "ga_kernel_launch_noalloc": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp]),
     "ga_mxfp8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
                            ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
     "ga_mxfp4_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,

@@ -914,6 +914,62 @@ ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int g
     return kernel_launch(idx, args, gdx, gdy, gdz, nullptr, 0, ws_handle, stream);
 }
 
+} // extern "C"
+
+namespace ga {
+
+// Split-K partials of ga_kernel_launch_noalloc: a fixed device array (each
+// GPU the library runs on holds its own copy until the process ends). Host
+// code never uses the array's name as an address: scratch_address() looks
+// the copy of the current device up once with hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+static ga_status scratch_address(float** out)
+{
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float* per_device[kMaxDevices] = {};
+    int dev = 0;
+    GA_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(GA_ERR_ARG, "kernel_launch_noalloc: device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_device[dev]) {
+        void* p = nullptr;
+        GA_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p)
+            return fail(GA_ERR_HIP, "kernel_launch_noalloc: no address for the scratch array");
+        per_device[dev] = (float*)p;
+    }
+    *out = per_device[dev];
+    return GA_OK;
+}
+
+} // namespace ga
+
+extern "C" {
+
+ga_status ga_kernel_launch_noalloc(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
+                                   int gdz, void* stream)
+{
+    if (!args)
+        return fail(GA_ERR_ARG, "kernel_launch_noalloc: null args");
+    float* ws = nullptr;
+    if (gdz > 1) {
+        const unsigned long long need =
+            (unsigned long long)gdz * args->M * args->N * sizeof(float);
+        if (need > kScratchBytes)
+            return fail(GA_ERR_WORKSPACE,
+                        "kernel_launch_noalloc: split-K partials need %llu bytes, the scratch "
+                        "holds %zu (gdz * M * N * 4 must fit)", need, kScratchBytes);
+        ga_status st = scratch_address(&ws);
+        if (st != GA_OK)
+            return st;
+    }
+    return kernel_launch(idx, args, gdx, gdy, gdz, ws, kScratchBytes, nullptr, stream);
+}
+
 ga_status ga_mxfp8_gemm(void* d_D, const void* d_A, const void* d_B, const void* d_ScaleA,
                         const void* d_ScaleB, int M, int N, int K, int stride_D0,
                         int bpreshuffle, int log2_k_split, int num_cu, void* workspace,

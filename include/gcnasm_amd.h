@@ -344,6 +344,19 @@ ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int g
                                      int gdz, const ga_splitk_ws_handle* ws_handle,
                                      void* stream);
 
+/* ga_kernel_launch for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc); no
+ * counterpart in the reference. Calls no hipMalloc/hipFree: with gdz > 1 the
+ * split-K partials [gdz, M, N] fp32 go to a fixed 32 MiB device array of the
+ * library (one per GPU it runs on, held until the process ends), so
+ * gdz * M * N * 4 must be at most 33554432 bytes (GA_ERR_WORKSPACE
+ * otherwise). Nothing in it needs to start at zero: every slice writes its
+ * whole partial before the reduce reads it. Every call on a GPU shares that
+ * array, so calls that overlap in time on one GPU (other streams, other host
+ * threads) race: serialise them. Otherwise as ga_kernel_launch. */
+ga_status ga_kernel_launch_noalloc(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
+                                   int gdz, void* stream);
+
 /* One-call MXFP8 GEMM: select_kernel + make_launch + fill_args + launch.
  * log2_k_split as in ga_select_kernel. Writes the chosen kernel index and
  * launch into *chosen / *ld_out when non-NULL. */

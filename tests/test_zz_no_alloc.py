@@ -1,0 +1,75 @@
+"""ga_kernel_launch_noalloc (split-K partials in the library's fixed device
+scratch array, no allocation) against ga_kernel_launch (caller workspace) on
+the same operands: bit-identical bf16 outputs, for two calls in a row, the
+second smaller than the first, and a call whose partials exceed the scratch
+is refused."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gcnasm_amd import _lib, f4gemm
+from helpers import mx_operands
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(dev, M, N, K, name, l2, seed):
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=seed)
+    sh = f4gemm.Shape(M, N, K)
+    a_pad = np.zeros((sh.a_rows_pad(), K), dtype=np.uint8)
+    a_pad[:M] = qa
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    bufs = [t(a_pad), t(f4gemm.shuffle_weight_16x16(qb, N, K)),
+            t(f4gemm.shuffle_scale(sa, M, K // 32, sh.scale_a_rows(), sh.scale_cols())),
+            t(f4gemm.shuffle_scale(sb, N, K // 32, sh.scale_b_rows(), sh.scale_cols()))]
+    cfg = [c for c in f4gemm.manifest() if c.knl_name == name][0]
+    ld = f4gemm.make_launch(cfg, M, N, K, l2)
+    outs = []
+    for _ in range(2):
+        D = torch.full((sh.d_rows_pad(), N), float("nan"), dtype=torch.bfloat16, device=dev)
+        args = f4gemm.fill_args(D, None, bufs[0], bufs[1], bufs[2], bufs[3], M, N, K, N,
+                                sh.scale_cols(), sh.scale_cols(), 1.0, 0.0, ld.log2_k_split)
+        outs.append((D, args))
+    idx = f4gemm.Kernel().load(None, cfg).idx
+    return idx, ld, outs, bufs
+
+
+def _bits(D, M):
+    return D[:M].view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_128x128_splitK",
+                                  "ga_mxfp8_bf16_BpreShuffle_64x256_splitK"])
+def test_noalloc_matches_workspace_launch(dev, name):
+    lib = _lib.lib()
+    for (M, N, K, l2, seed) in ((512, 2048, 4096, 2, 1), (256, 1024, 2048, 1, 2)):
+        idx, ld, outs, bufs = _problem(dev, M, N, K, name, l2, seed)
+        assert ld.gdz == 1 << l2
+        (D0, a0), (D1, a1) = outs
+        ws = torch.empty(ld.gdz * M * N, dtype=torch.float32, device=dev)
+        print("noalloc %s M=%d N=%d K=%d gdz=%d" % (name, M, N, K, ld.gdz), flush=True)
+        _lib.check(lib.ga_kernel_launch(idx, ctypes.byref(a0), ld.gdx, ld.gdy, ld.gdz,
+                                        ws.data_ptr(), ws.numel() * 4, None))
+        _lib.check(lib.ga_kernel_launch_noalloc(idx, ctypes.byref(a1), ld.gdx, ld.gdy, ld.gdz,
+                                                None))
+        torch.cuda.synchronize()
+        want = _bits(D0, M)
+        got = _bits(D1, M)
+        assert not np.any(np.isnan(oracle.bf16_bits_to_f32(got)))
+        np.testing.assert_array_equal(got, want)
+        del ws, outs, bufs
+
+
+def test_noalloc_rejects_partials_beyond_the_scratch(dev):
+    lib = _lib.lib()
+    M, N, K, l2 = 2048, 4096, 1024, 1  # 2 * 2048 * 4096 * 4 = 64 MiB > 32 MiB
+    name = "ga_mxfp8_bf16_BpreShuffle_256x256_splitK"
+    idx, ld, outs, bufs = _problem(dev, M, N, K, name, l2, 3)
+    st = lib.ga_kernel_launch_noalloc(idx, ctypes.byref(outs[0][1]), ld.gdx, ld.gdy, ld.gdz,
+                                      None)
+    assert st == _lib.GA_ERR_WORKSPACE
+    torch.cuda.synchronize()
