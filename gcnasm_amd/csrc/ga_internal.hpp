@@ -33,6 +33,7 @@ struct MxKernel {
     mx_launch_fn launch;
     int small_m_stream; // M up to this many rows goes to the decode path (launch_mx_decode)
     int elem_bits;      // 8: E4M3 operands, 4: e2m1 packed two per byte
+    bool by_shape;      // a tile known by name: runs the compiled tile the heuristic picks
 };
 // 256x256 eight-wave kernels (gemm_mx_pp.hip), preshuffled / plain B.
 void launch_mx_pp_bps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,

@@ -39,8 +39,12 @@
 #include "ga_internal.hpp"
 #include "ga_pp.hpp"
 
+#include <atomic>
+#include <cstdio>
 #include <cstring>
+#include <deque>
 #include <mutex>
+#include <string>
 #include <vector>
 
 namespace ga {
@@ -642,6 +646,23 @@ static void launch_mxb(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_w
       "ga_mxfp4_bf16_" GA_BPS_NAME_##BPS "_256x256" SUFFIX ".co"},                              \
      &FN, 64, 4}
 
+// Tiles found by name only, as the reference's aiter manifest names them
+// (35 tiles, e.g. 96x640 and 128x512): the entry's tile fixes the launch
+// contract the caller sees (the grid ceil(N/tN) x ceil(M/tM) x gdz that
+// make_launch returns and kernel_launch checks, the split geometry, the
+// workspace); the kernel that runs is the one the heuristic picks for the
+// shape among this element width's compiled tiles at the same split. Every
+// compiled tile computes the same fp32 chain per K slice, so the output does
+// not depend on that choice.
+template <bool BPS, bool FP4>
+static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                            int gdx, int gdy, int gdz, hipStream_t stream);
+
+#define GA_MXV_ENTRY(PREFIX, EB, FP4, BM, BN, SPLIT, SUFFIX)                                  \
+    {{BM, BN, SPLIT, 1, PREFIX "_BpreShuffle_" #BM "x" #BN SUFFIX,                            \
+      PREFIX "_BpreShuffle_" #BM "x" #BN SUFFIX ".co"},                                       \
+     &launch_by_shape<true, FP4>, 64, EB, true}
+
 static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(1, 0, "", launch_mx_pp_bps),
     GA_MX_ENTRY(256, 128, 2, 2, 1, 3, 0, ""),
@@ -659,6 +680,11 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX_PP_ENTRY(0, 0, "", launch_mx_pp_nobps),
     GA_MX_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
     GA_MX_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
+    // tiles of the reference's MXFP4 manifest this one did not have
+    GA_MXV_ENTRY("ga_mxfp8_bf16", 8, false, 96, 640, 0, ""),
+    GA_MXV_ENTRY("ga_mxfp8_bf16", 8, false, 128, 512, 0, ""),
+    GA_MXV_ENTRY("ga_mxfp8_bf16", 8, false, 96, 640, 1, "_splitK"),
+    GA_MXV_ENTRY("ga_mxfp8_bf16", 8, false, 128, 512, 1, "_splitK"),
     // not in the manifest: the 4-wave 256x256 tile (two stages)
     GA_MX_ENTRY(256, 256, 2, 2, 1, 2, 0, "_ns2"),
     // the MXFP4 manifest, the MXFP8 one's tiles and order
@@ -678,16 +704,146 @@ static const MxKernel g_mx_kernels[] = {
     GA_MX4_PP_ENTRY(0, 0, "", launch_mx4_pp_nobps),
     GA_MX4_ENTRY(256, 128, 2, 2, 0, 3, 0, ""),
     GA_MX4_ENTRY(128, 128, 2, 2, 0, 2, 1, "_splitK"),
+    GA_MXV_ENTRY("ga_mxfp4_bf16", 4, true, 96, 640, 0, ""),
+    GA_MXV_ENTRY("ga_mxfp4_bf16", 4, true, 128, 512, 0, ""),
+    GA_MXV_ENTRY("ga_mxfp4_bf16", 4, true, 96, 640, 1, "_splitK"),
+    GA_MXV_ENTRY("ga_mxfp4_bf16", 4, true, 128, 512, 1, "_splitK"),
 };
-constexpr int kManifestCount = 16;
-constexpr int kMx4First = 17;
-constexpr int kMx4Count = 16;
+constexpr int kManifestCount = 20;
+constexpr int kMx4First = 21;
+constexpr int kMx4Count = 20;
+constexpr int kStaticCount = (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0]));
+static_assert(kMx4First + kMx4Count == kStaticCount, "registry layout");
+
+// Entries made by ga_kernel_find from a tile name (aiter's
+// f4gemm_bf16_per1x32Fp4_[no]BpreShuffle_<tM>x<tN>, or this library's
+// ga_mxfp{8,4}_bf16_... with any tile): indices kStaticCount and up. A deque
+// keeps earlier entries in place as it grows.
+static std::mutex g_named_mu;
+static std::deque<MxKernel> g_named;
+static std::atomic<int> g_named_count{0};
 
 int mx_registry_count() { return kManifestCount; }
 int mx4_registry_first() { return kMx4First; }
 int mx4_registry_count() { return kMx4Count; }
-int mx_registry_total() { return (int)(sizeof(g_mx_kernels) / sizeof(g_mx_kernels[0])); }
-const MxKernel* mx_registry_get(int idx) { return &g_mx_kernels[idx]; }
+int mx_registry_total() { return kStaticCount + g_named_count.load(std::memory_order_acquire); }
+const MxKernel* mx_registry_get(int idx)
+{
+    if (idx < kStaticCount)
+        return &g_mx_kernels[idx];
+    std::lock_guard<std::mutex> lock(g_named_mu);
+    return &g_named[idx - kStaticCount];
+}
+
+template <bool BPS, bool FP4>
+static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                            int gdx, int gdy, int gdz, hipStream_t stream)
+{
+    (void)gdx;
+    (void)gdy;
+    const int first = FP4 ? kMx4First : 0, count = FP4 ? kMx4Count : kManifestCount;
+    ga_tile_config table[kManifestCount];
+    int map[kManifestCount], n = 0;
+    for (int i = first; i < first + count; i++)
+        if (!g_mx_kernels[i].by_shape) {
+            map[n] = i;
+            table[n++] = g_mx_kernels[i].cfg;
+        }
+    int num_cu = 0;
+    if (device_cu_count(&num_cu) != GA_OK || num_cu <= 0)
+        num_cu = 256;
+    int row = -1, l2 = 0;
+    const int L = gdz > 1 ? args.log2_k_split : 0;
+    int idx = map[0]; // the 256x256 tile of this width takes any shape
+    if (!BPS)
+        for (int i = 0; i < n; i++)
+            if (!table[i].bpreshuffle && table[i].tile_M == 256 && table[i].tile_N == 256)
+                idx = map[i];
+    if (ga_select_kernel((int)args.M, (int)args.N, (int)args.K, num_cu, L, BPS ? 1 : 0, table, n,
+                         &row, &l2) == GA_OK &&
+        row >= 0)
+        idx = map[row];
+    const MxKernel& k = g_mx_kernels[idx];
+    k.launch(args, ws, wsh, ((int)args.N + k.cfg.tile_N - 1) / k.cfg.tile_N,
+             ((int)args.M + k.cfg.tile_M - 1) / k.cfg.tile_M, gdz, stream);
+}
+
+// Parses a tile name into a by-shape entry; false when it is not one.
+static bool parse_tile_name(const char* name, MxKernel* out)
+{
+    std::string s(name);
+    const bool mangled = s.compare(0, 2, "_Z") == 0;
+    if (s.size() > 3 && s.compare(s.size() - 3, 3, ".co") == 0)
+        s.resize(s.size() - 3);
+    struct Family {
+        const char* prefix;
+        int elem_bits;
+        bool aiter;
+    };
+    static const Family fams[] = {{"f4gemm_bf16_per1x32Fp4_", 4, true},
+                                  {"ga_mxfp4_bf16_", 4, false},
+                                  {"ga_mxfp8_bf16_", 8, false}};
+    const Family* f = nullptr;
+    size_t at = std::string::npos;
+    for (const Family& c : fams) {
+        at = s.find(c.prefix);
+        if (at != std::string::npos && (at == 0 || mangled)) {
+            f = &c;
+            break;
+        }
+    }
+    if (!f)
+        return false;
+    std::string rest = s.substr(at + strlen(f->prefix));
+    int bps;
+    if (rest.compare(0, 12, "BpreShuffle_") == 0) {
+        bps = 1;
+        rest = rest.substr(12);
+    } else if (rest.compare(0, 14, "noBpreShuffle_") == 0) {
+        bps = 0;
+        rest = rest.substr(14);
+    } else {
+        return false;
+    }
+    int tm = 0, tn = 0, used = 0;
+    if (sscanf(rest.c_str(), "%dx%d%n", &tm, &tn, &used) != 2)
+        return false;
+    std::string tail = rest.substr(used);
+    int split;
+    if (f->aiter) {
+        // aiter's names do not mark split-K (its CSV's splitK column does)
+        if (!(tail.empty() || (mangled && tail == "E")))
+            return false;
+        split = 1;
+    } else {
+        if (tail == "_splitK")
+            split = 1;
+        else if (tail.empty())
+            split = 0;
+        else
+            return false;
+    }
+    if (tm < 16 || tn < 16 || tm > 1024 || tn > 1024 || tm % 16 || tn % 16)
+        return false;
+    if (strlen(name) >= GA_NAME_MAX)
+        return false;
+    MxKernel k{};
+    k.cfg.tile_M = tm;
+    k.cfg.tile_N = tn;
+    k.cfg.splitK = split;
+    k.cfg.bpreshuffle = bps;
+    snprintf(k.cfg.knl_name, GA_NAME_MAX, "%s", name);
+    if (snprintf(k.cfg.co_name, GA_NAME_MAX, "%s.co", s.c_str()) >= GA_NAME_MAX)
+        return false;
+    const bool fp4 = f->elem_bits == 4;
+    k.launch = fp4 ? (bps ? &launch_by_shape<true, true> : &launch_by_shape<false, true>)
+                   : (bps ? &launch_by_shape<true, false> : &launch_by_shape<false, false>);
+    k.small_m_stream = 64;
+    k.elem_bits = f->elem_bits;
+    k.by_shape = true;
+    *out = k;
+    return true;
+}
 
 ga_status default_workspace(size_t bytes, void** ptr)
 {
@@ -723,15 +879,31 @@ ga_status ga_kernel_find(const char* name, int* idx)
 {
     if (!name || !idx)
         return fail(GA_ERR_ARG, "null argument");
-    for (int i = 0; i < mx_registry_total(); i++) {
+    for (int i = 0; i < kStaticCount; i++) {
         const ga_tile_config& c = g_mx_kernels[i].cfg;
         if (!strcmp(c.knl_name, name) || !strcmp(c.co_name, name)) {
             *idx = i;
             return GA_OK;
         }
     }
-    *idx = -1;
-    return fail(GA_ERR_NO_KERNEL, "kernel '%s' not in the manifest", name);
+    MxKernel k;
+    const bool parsed = parse_tile_name(name, &k);
+    std::lock_guard<std::mutex> lock(g_named_mu);
+    for (size_t i = 0; i < g_named.size(); i++) {
+        const ga_tile_config& c = g_named[i].cfg;
+        if (!strcmp(c.knl_name, name) || !strcmp(c.co_name, name)) {
+            *idx = kStaticCount + (int)i;
+            return GA_OK;
+        }
+    }
+    if (!parsed) {
+        *idx = -1;
+        return fail(GA_ERR_NO_KERNEL, "kernel '%s' not in the manifest", name);
+    }
+    g_named.push_back(k);
+    g_named_count.store((int)g_named.size(), std::memory_order_release);
+    *idx = kStaticCount + (int)g_named.size() - 1;
+    return GA_OK;
 }
 
 size_t ga_kernel_workspace_bytes(int idx, const ga_launch_desc* ld, int M, int N)
@@ -755,7 +927,7 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
 {
     if (!args || idx < 0 || idx >= mx_registry_total())
         return fail(GA_ERR_ARG, "kernel_launch: bad kernel index %d", idx);
-    const MxKernel& k = g_mx_kernels[idx];
+    const MxKernel& k = *mx_registry_get(idx);
     const int M = (int)args->M, N = (int)args->N, K = (int)args->K;
     if (M <= 0 || N <= 0 || K <= 0 || !args->ptr_A || !args->ptr_B || !args->ptr_D ||
         !args->ptr_ScaleA || !args->ptr_ScaleB)

@@ -80,7 +80,26 @@ FP4_MANIFEST = ["ga_mxfp4_bf16_BpreShuffle_%s" % t for t in
                ["ga_mxfp4_bf16_BpreShuffle_%s_splitK" % t for t in
                 ("256x256", "256x128", "128x256", "128x128", "64x256", "32x256", "32x512")] + \
                ["ga_mxfp4_bf16_noBpreShuffle_256x256", "ga_mxfp4_bf16_noBpreShuffle_256x128",
-                "ga_mxfp4_bf16_noBpreShuffle_128x128_splitK"]
+                "ga_mxfp4_bf16_noBpreShuffle_128x128_splitK"] + \
+               ["ga_mxfp4_bf16_BpreShuffle_96x640", "ga_mxfp4_bf16_BpreShuffle_128x512",
+                "ga_mxfp4_bf16_BpreShuffle_96x640_splitK",
+                "ga_mxfp4_bf16_BpreShuffle_128x512_splitK"]
+
+# Tile names in the reference's own (aiter) form: the ones its files name
+# (asm_f4gemm/README.md:25-31 and :174, run_tests.sh:51-52) and more shapes of
+# that naming; ga_kernel_find resolves each (the tile fixes the grid and the
+# split contract; the library runs its own compiled tile for the shape).
+AITER_TILES = ["BpreShuffle_256x256", "BpreShuffle_96x640", "BpreShuffle_128x512",
+               "noBpreShuffle_256x256", "BpreShuffle_32x128", "BpreShuffle_64x384",
+               "BpreShuffle_160x256", "BpreShuffle_224x256", "BpreShuffle_192x128"]
+
+
+def aiter_cfg(tile):
+    import re
+    m = re.search(r"(\d+)x(\d+)$", tile)
+    name = "f4gemm_bf16_per1x32Fp4_%s.co" % tile
+    return f4gemm.Config(int(m.group(1)), int(m.group(2)), 1, int(not tile.startswith("no")),
+                         name, name)
 
 
 def test_manifest_fp4_rows():
@@ -100,6 +119,27 @@ def test_every_fp4_kernel(dev, name):
     got = run_mx4(dev, qa, sa, qb, sb, cfg4(name))
     st = check4(got, qa, sa, qb, sb, 0, name)
     assert st["exact"] > 0.95
+
+
+@pytest.mark.parametrize("tile", AITER_TILES)
+def test_aiter_tile_names(dev, tile):
+    """Every manifest kernel at M=300 N=2048 K=1024 (run_tests.sh:43-49),
+    found by its aiter name."""
+    M, N, K = 300, 2048, 1024
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=3)
+    got = run_mx4(dev, qa, sa, qb, sb, aiter_cfg(tile))
+    check4(got, qa, sa, qb, sb, 0, "aiter %s" % tile)
+
+
+@pytest.mark.parametrize("tile", ["BpreShuffle_256x256", "BpreShuffle_128x512"])
+@pytest.mark.parametrize("l2", [1, 2, 3, 4])
+def test_aiter_tile_splitk(dev, tile, l2):
+    """The reference's split-K sweep (run_tests.sh:51-57): M=256 N=1024 K=4096
+    with log2_k_split 1..4 on its 256x256 and 128x512 tiles."""
+    M, N, K = 256, 1024, 4096
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=20 + l2)
+    got = run_mx4(dev, qa, sa, qb, sb, aiter_cfg(tile), l2)
+    check4(got, qa, sa, qb, sb, l2, "aiter %s L=%d" % (tile, l2))
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 512), (1, 512, 256), (17, 784, 1280),
