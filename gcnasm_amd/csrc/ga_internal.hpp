@@ -51,6 +51,14 @@ void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz);
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,
                       hipStream_t stream);
+// 17-64 rows, each wave over ng (2-8) 16-column groups and one K slice, the
+// slices in separate workgroups (gemm_mx_decode.hip): mx_decode_split_groups
+// gives ng for the shape (0: not this path); with gdz > 1 the slices write
+// fp32 partials to the split-K workspace (ws, or the slot wsh) for the
+// split-K reduce, with gdz = 1 the kernel applies the epilogue.
+int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu);
+void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
+                            float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream);
 
 // Compute units of the current device (queried once per device).
 ga_status device_cu_count(int* num_cu);

@@ -982,30 +982,21 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
     }
     hipStream_t s = (hipStream_t)stream;
     // a caller workspace is checked against ga_kernel_workspace_bytes whichever
-    // path runs (the decode path sums K slices in LDS and needs none)
+    // path runs (the in-workgroup decode kernel sums K slices in LDS and needs
+    // none)
     if (gdz > 1 && workspace && workspace_bytes < (size_t)gdz * M * N * sizeof(float))
         return fail(GA_ERR_WORKSPACE, "workspace %zu bytes, need %zu", workspace_bytes,
                     (size_t)gdz * M * N * sizeof(float));
-    if ((int)args->M <= k.small_m_stream && mx_decode_applies(*args, gdz)) {
-        // few rows: stream B, K slices summed inside the kernel (no workspace)
-        int num_cu = 0;
+    const bool decode = (int)args->M <= k.small_m_stream && mx_decode_applies(*args, gdz);
+    int num_cu = 0;
+    if (decode) {
         ga_status st = device_cu_count(&num_cu);
         if (st != GA_OK)
             return st;
-        // 33-64 rows over wide N (32x256 B-streaming tiles covering 3/4 of
-        // the CUs): those tiles load A once per 256 columns where the decode
-        // kernel's waves load it per 32 (measured on MI355X, M = 64,
-        // N = 28672, K = 8192: 75.8 -> 38.9 us MXFP8, 41.5 -> 23.8 us MXFP4;
-        // with fewer tiles the decode kernel's K slices win)
-        const long long wide = (long long)((M + 31) / 32) * ((N + 255) / 256);
-        if (gdz == 1 && M > 32 && k.cfg.bpreshuffle && wide * 4 >= 3LL * num_cu) {
-            if (k.elem_bits == 4)
-                launch_mxb<MbCfg<32, 256, 4, true>>(*args, nullptr, nullptr, 0, (M + 31) / 32, 1, s);
-            else
-                launch_mxb<MbCfg<32, 256, 4, false>>(*args, nullptr, nullptr, 0, (M + 31) / 32, 1, s);
-            GA_HIP_CHECK(hipGetLastError());
-            return GA_OK;
-        }
+    }
+    const int split_groups = decode ? mx_decode_split_groups(*args, gdz, num_cu) : 0;
+    if (decode && split_groups == 0) {
+        // few rows: stream B, K slices summed inside the kernel (no workspace)
         launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, num_cu, s);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;
@@ -1041,7 +1032,11 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
             ws = (float*)p;
         }
     }
-    k.launch(*args, ws, gdz > 1 ? wsh : nullptr, gdx, gdy, gdz, s);
+    if (split_groups > 0)
+        launch_mx_decode_split(*args, gdz, split_groups, k.cfg.bpreshuffle != 0, k.elem_bits == 4,
+                               ws, wsh, s);
+    else
+        k.launch(*args, ws, gdz > 1 ? wsh : nullptr, gdx, gdy, gdz, s);
     GA_HIP_CHECK(hipGetLastError());
     if (gdz > 1) {
         ReduceArgs r;

@@ -19,6 +19,19 @@
 //  * MXFP4 (e2m1 packed two per byte): a step is 256 K = the same 128 bytes
 //    per row, so the loads are identical; two fp4 MFMAs per group and 16
 //    rows (K halves 0 and 1 of the step), one whole scale dword per step.
+//  * split variant (XS; 17-64 rows with the caller's gdz > 1, or one slice
+//    over N wide enough for five groups per CU): the K slice is blockIdx.y
+//    and each wave owns NG (2-8) groups, so a CU reads A once per up to 128
+//    columns instead of once per 32 (at 64 rows and NG = 8, A is half the
+//    bytes of B rather than twice); waves x slices fill whole rounds of one
+//    wave per CU. The slices' fp32 partials go to the split-K workspace and
+//    the split-K reduce sums them in slice order, slice 0 first, as above;
+//    one slice applies the epilogue in the kernel. Measured on MI355X, M =
+//    64, N = 8192, K = 28672: 70 us in-workgroup at any split, 45.9 us here
+//    at 4 slices (41.9 us kernel + 4 us reduce); N = 28672, K = 8192, one
+//    slice: 65 -> 54.7 us. Each group's next B loads go out right after the
+//    MFMAs of the following group, so they never wait on an MFMA still
+//    reading their registers and the wave's requests spread over its MFMAs.
 #include "ga_device.hpp"
 #include "ga_internal.hpp"
 #include <algorithm>
@@ -29,42 +42,64 @@ namespace {
 // DEEP: up to 4 waves per workgroup, so each may use 512 registers and keep
 // more steps in flight (4 of 64 rows, 6 of 32 rows; for long K with one
 // column task per CU).
-template <int TM, int NG_, bool DEEP = false>
+// XS > 0: the cross-workgroup split with XS steps in flight, one wave per
+// SIMD (512 registers).
+template <int TM, int NG_, bool DEEP = false, int XS = 0>
 struct DecCfg {
     static constexpr int NG = NG_; // 16-column groups per wave
-    static constexpr int D = DEEP ? (TM == 4 ? 4 : 6)
+    static constexpr int D = XS > 0 ? XS
+                           : DEEP ? (TM == 4 ? 4 : 6)
                                   : TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
-    static constexpr int MAX_WAVES = DEEP ? 4 : 8;
+    static constexpr int MAX_WAVES = (DEEP || XS > 0) ? 4 : 8;
+    // B scale dwords per step: a wave of the split variant with an even NG
+    // starts at an even group, so groups 2j and 2j + 1 share the dword of one
+    // 32-row block
+    static constexpr int NB = (XS > 0 && NG % 2 == 0) ? NG / 2 : NG;
 };
 
 // Uniform byte offsets as SGPR operands.
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-template <int TM, int NG_, bool BPS, bool FP4, bool DEEP>
-__global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP>::MAX_WAVES * 64)))
-void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
+template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0>
+__global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP, XS>::MAX_WAVES * 64)))
+void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__ ws,
+                      const ga_splitk_ws_handle* __restrict__ wsh)
 {
+    using Cfg = DecCfg<TM, NG_, DEEP, XS>;
     constexpr int kEPB = FP4 ? 2 : 1; // elements per byte
-    constexpr int D = DecCfg<TM, NG_, DEEP>::D, NG = NG_, NB = NG; // one scale dword per group
+    constexpr int D = Cfg::D, NG = NG_, NB = Cfg::NB;
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
     constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
     static_assert(kLoadsPerStep * (D - 1) < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(16))) float red[8 * NG * TM * 256]; // <= 8 waves
+    // in-workgroup K slices are summed through LDS (<= 8 waves)
+    __shared__ __attribute__((aligned(16))) float red[XS > 0 ? 4 : 8 * NG * TM * 256];
+    if constexpr (XS > 0) {
+        if (gridDim.y > 1 && wsh && !(ws = resolve_ws(wsh, gridDim.y, args.M, args.N)))
+            return; // workspace slot shorter than the split-K layout: write nothing
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int slice = wave % ks, tl = wave / ks;
+    const int slice = XS > 0 ? (int)blockIdx.y : wave % ks;
+    const int tl = XS > 0 ? wave : wave / ks;
     const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
     // Workgroup b owns 16-column groups [b*G/nwg, (b+1)*G/nwg): equal shares
-    // (within one group) for every CU; its waves take NG groups each.
+    // (within one group) for every CU; its waves take NG groups each. In the
+    // split variant wave w of workgroup b takes groups from (b*waves + w)*NG.
     const int ngroups = N / 16;
-    const int g_end = (int)(((long long)(blockIdx.x + 1) * ngroups) / nwg);
-    const int cg0 = (int)(((long long)blockIdx.x * ngroups) / nwg) + tl * NG;
+    int g_end, cg0;
+    if constexpr (XS > 0) {
+        g_end = ngroups;
+        cg0 = ((int)blockIdx.x * (int)(blockDim.x >> 6) + tl) * NG;
+    } else {
+        g_end = (int)(((long long)(blockIdx.x + 1) * ngroups) / nwg);
+        cg0 = (int)(((long long)blockIdx.x * ngroups) / nwg) + tl * NG;
+    }
     const int ng_here = min(NG, g_end - cg0); // groups past it read as zero
     const bool live = ng_here > 0;
 
     int kpt = K;
-    if (ks > 1)
+    if (XS > 0 ? gridDim.y > 1 : ks > 1)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
     const int kb = slice * kpt;
     const int ke = min(K, kb + kpt);
@@ -112,11 +147,14 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
         const auto rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)((M + 31) / 32 * 32) * sna);
         const auto rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)((N + 31) / 32 * 32) * snb);
         const uint32_t vsa = ((uint32_t)(kb / 256)) * 256 + lane * 4;
-        // group cg uses byte (cg & 1) of 32-row block cg/2
-        uint32_t vsb[NG];
+        // group cg uses byte (cg & 1) of 32-row block cg/2 (one dword per
+        // group, or per group pair in the split variant)
+        uint32_t vsb[NB];
 #pragma unroll
-        for (int c = 0; c < NG; c++)
-            vsb[c] = ((uint32_t)((cg0 + c) / 2) * (snb / 8) + (uint32_t)(kb / 256)) * 256 + lane * 4;
+        for (int c = 0; c < NB; c++) {
+            const int cg = NB == NG ? cg0 + c : cg0 + 2 * c;
+            vsb[c] = ((uint32_t)(cg / 2) * (snb / 8) + (uint32_t)(kb / 256)) * 256 + lane * 4;
+        }
         const uint32_t sa_blk = (sna / 8) * 256;
 
         v8i fb[D][NG];
@@ -152,7 +190,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
             const uint32_t sh = FP4 ? 0u : (uint32_t)(s & 1) * 16;
 #pragma unroll
             for (int c = 0; c < NG; c++) {
-                const uint32_t sb = fsb[j][c] >> (sh + 8 * ((cg0 + c) & 1));
+                const uint32_t sb = fsb[j][NB == NG ? c : c / 2] >> (sh + 8 * ((cg0 + c) & 1));
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
                     const uint32_t sa = fsa[j][i >> 1] >> (sh + 8 * (i & 1));
@@ -169,6 +207,66 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
             }
         };
 
+        // Split variant: step s's MFMAs group by group, the B loads of group
+        // c - 1 for step sn issued after group c's MFMAs (the MFMAs reading
+        // group c - 1's registers are done by then, so the loads do not wait
+        // on them): the wave's memory requests spread over the MFMA block
+        // instead of following it. Then A and the scales, in load()'s order.
+        auto mma_load = [&](int s, int sn, auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t sh = FP4 ? 0u : (uint32_t)(s & 1) * 16;
+            uint32_t sav[SA], sbv[NB];
+#pragma unroll
+            for (int h = 0; h < SA; h++)
+                sav[h] = fsa[j][h];
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+                sbv[c] = fsb[j][c];
+            const uint32_t ob = (uint32_t)sn * b_step;
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                const uint32_t sb = sbv[NB == NG ? c : c / 2] >> (sh + 8 * ((cg0 + c) & 1));
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const uint32_t sa = sav[i >> 1] >> (sh + 8 * (i & 1));
+                    if constexpr (FP4) {
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
+                                                        (int)sa);
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(hi16(fb[j][c]), hi16(fa[j][i]), acc[c][i],
+                                                        (int)(sb >> 16), (int)(sa >> 16));
+                    } else {
+                        acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
+                                                    (int)sa);
+                    }
+                }
+                if (c > 0) {
+                    v4i x0 = buf_load16_stream(rbuf, vb + uni(ob + (c - 1) * b_grp), 0);
+                    v4i x1 = buf_load16_stream(rbuf, vb + uni(ob + (c - 1) * b_grp + b_hi), 0);
+                    fb[j][c - 1] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                v4i x0 = buf_load16_stream(rbuf, vb + uni(ob + (NG - 1) * b_grp), 0);
+                v4i x1 = buf_load16_stream(rbuf, vb + uni(ob + (NG - 1) * b_grp + b_hi), 0);
+                fb[j][NG - 1] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const uint32_t oa = (uint32_t)sn * 128 + (uint32_t)i * 16 * lda;
+                v4i y0 = buf_load16(ra, va + uni(oa), 0);
+                v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
+                fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+            }
+            const uint32_t q = (uint32_t)(FP4 ? sn : (sn >> 1)) * 256;
+#pragma unroll
+            for (int h = 0; h < SA; h++)
+                fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
+#pragma unroll
+            for (int c = 0; c < NB; c++)
+                fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+        };
+
         // The loads of each step stay in issue order (slot 0 oldest), so the
         // wait before step s+J's MFMAs lets the D-1 younger steps fly.
         static_for<D>([&](auto J) {
@@ -179,8 +277,12 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
         for (; s + D <= nsteps; s += D) {
             static_for<D>([&](auto J) {
                 wait_vmcnt<kLoadsPerStep * (D - 1)>();
-                mma(s + J, J);
-                load(min(s + D + (int)J, nsteps - 1), J);
+                if constexpr (XS > 0) {
+                    mma_load(s + J, min(s + D + (int)J, nsteps - 1), J);
+                } else {
+                    mma(s + J, J);
+                    load(min(s + D + (int)J, nsteps - 1), J);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
@@ -190,9 +292,28 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks)
         });
     }
 
-    // Sum the K slices of each column group in slice order, then the epilogue
-    // (lane holds C[m][n .. n+3], m = 16i + lane%16, n = 16cg + 4(lane/16)).
-    if (ks > 1) {
+    // Split variant: this slice's fp32 partials to the workspace, [slice][M][N]
+    // (lane holds C[m][n .. n+3], m = 16i + lane%16, n = 16cg + 4(lane/16));
+    // one slice: the epilogue below.
+    if (XS > 0 && gridDim.y > 1) {
+        if (!live)
+            return;
+#pragma unroll
+        for (int c = 0; c < NG; c++) {
+            if (c >= ng_here)
+                continue;
+            const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int m = i * 16 + (lane & 15);
+                if (m < M)
+                    *(v4f*)(ws + ((size_t)slice * M + m) * N + n) = acc[c][i];
+            }
+        }
+        return;
+    }
+    // Sum the K slices of each column group in slice order, then the epilogue.
+    if (XS == 0 && ks > 1) {
         float* mine = red + ((tl * ks + slice) * NG * TM) * 256;
 #pragma unroll
         for (int c = 0; c < NG; c++)
@@ -261,7 +382,45 @@ void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t str
     const int share = (groups + nwg - 1) / nwg;
     const int tasks = (share + NG - 1) / NG;
     hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP>), dim3(nwg), dim3(64 * tasks * ks), 0,
-                       stream, args, nwg, ks);
+                       stream, args, nwg, ks, nullptr, nullptr);
+}
+
+// Split variant: one wave of NG groups per workgroup per K slice, grid
+// (tasks, gdz); partials to ws (or the slot wsh) for the split-K reduce, or
+// with one slice the epilogue in the kernel. Steps in flight: as many as the
+// 63 outstanding loads a wave can count allow, at most 4.
+template <int TM, int NG, bool FP4>
+constexpr int xs_depth()
+{
+    constexpr int nb = NG % 2 == 0 ? NG / 2 : NG;
+    constexpr int loads = 2 * NG + 2 * TM + (TM + 1) / 2 + nb;
+    return 1 + 63 / loads > 4 ? 4 : 1 + 63 / loads;
+}
+
+template <int TM, int NG, bool BPS, bool FP4>
+void launch_dec_xs(const ga_f4gemm_kargs& args, int gdz, float* ws, const ga_splitk_ws_handle* wsh,
+                   hipStream_t stream)
+{
+    const int groups = (int)args.N / 16;
+    const int tasks = (groups + NG - 1) / NG;
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, false, xs_depth<TM, NG, FP4>()>),
+                       dim3(tasks, gdz), dim3(64), 0, stream, args, tasks, 1, ws, wsh);
+}
+
+template <int TM, bool BPS, bool FP4>
+void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
+                      const ga_splitk_ws_handle* wsh, hipStream_t stream)
+{
+    if (!BPS) // row-major B: the two extremes only
+        ng = ng <= 2 ? 2 : 8;
+    switch (ng) {
+    case 2: launch_dec_xs<TM, 2, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    case 4: launch_dec_xs<TM, 4, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    case 5: launch_dec_xs<TM, 5, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    case 6: launch_dec_xs<TM, 6, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    case 7: launch_dec_xs<TM, 7, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    default: launch_dec_xs<TM, 8, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    }
 }
 
 template <bool BPS, bool FP4>
@@ -303,6 +462,45 @@ void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz)
 {
     return args.M >= 1 && args.M <= 64 && gdz <= 8;
+}
+
+int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
+{
+    if (args.M <= 16 || args.M > 64 || gdz > 8 || num_cu <= 0)
+        return 0;
+    // waves (tasks x slices) in whole rounds of one per CU, as few rounds as
+    // eight groups per wave allow, the groups spread evenly over them
+    // (N = 28672, one slice: 7 groups, 256 waves; N = 8192, 4 slices: 8)
+    const long long work = (long long)(args.N / 16) * gdz;
+    const long long rounds = (work + 8LL * num_cu - 1) / (8LL * num_cu);
+    int ng = (int)((work + rounds * num_cu - 1) / (rounds * num_cu));
+    ng = ng < 2 ? 2 : (ng == 3 ? 4 : ng);
+    // one slice: only when a wave gets at least five groups (narrower N
+    // keeps the in-workgroup kernel, which needs no partials either way)
+    if (gdz == 1 && ng < 5)
+        return 0;
+    return ng;
+}
+
+void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
+                            float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream)
+{
+    const bool rows64 = args.M > 32;
+    if (fp4) {
+        if (bps)
+            rows64 ? launch_dec_xs_ng<4, true, true>(args, gdz, ng, ws, wsh, stream)
+                   : launch_dec_xs_ng<2, true, true>(args, gdz, ng, ws, wsh, stream);
+        else
+            rows64 ? launch_dec_xs_ng<4, false, true>(args, gdz, ng, ws, wsh, stream)
+                   : launch_dec_xs_ng<2, false, true>(args, gdz, ng, ws, wsh, stream);
+    } else {
+        if (bps)
+            rows64 ? launch_dec_xs_ng<4, true, false>(args, gdz, ng, ws, wsh, stream)
+                   : launch_dec_xs_ng<2, true, false>(args, gdz, ng, ws, wsh, stream);
+        else
+            rows64 ? launch_dec_xs_ng<4, false, false>(args, gdz, ng, ws, wsh, stream)
+                   : launch_dec_xs_ng<2, false, false>(args, gdz, ng, ws, wsh, stream);
+    }
 }
 
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,

@@ -307,6 +307,59 @@ def test_decode_deep_k_split(dev, MNKL):
           (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
+# (N, K, log2 split) -> 16-column groups per wave on 256 CUs, slices: every
+# groups-per-wave instantiation, ragged last waves, whole rounds of waves.
+SPLIT_DECODE_SHAPES = [
+    (1040, 4096, 2),        # 65 groups x 4 slices: 2 groups, last wave holds one
+    (8192 + 48, 2048, 3),   # 515 groups x 8: 6 groups, three rounds
+    (4096, 1152, 1),        # 2 groups; second slice shorter (768 + 384)
+    (8192, 2048, 1),        # 4 groups
+    (8192, 2048, 2),        # 8 groups
+    (19216, 512, 0),        # one slice, 1201 groups: 5 per wave, last holds one
+    (22400, 512, 0),        # one slice: 6 groups
+    (28672 - 16, 512, 0),   # one slice: 7 groups, last wave holds six
+    (28672 - 16, 1024, 1),  # 2 slices x 1791 groups: 7 groups, two rounds
+    (19216, 2048, 2),       # 4 slices x 1201 groups: 5 groups, four rounds
+    (22400, 1152, 1),       # 2 slices of 768 + 384: 6 groups
+    (28672 - 16, 2048, 3),  # 8 slices: 8 groups, seven rounds
+]
+
+
+@pytest.mark.parametrize("M", [20, 40, 64])
+@pytest.mark.parametrize("bps", [True, False])
+@pytest.mark.parametrize("NKL", SPLIT_DECODE_SHAPES)
+def test_decode_split_across_workgroups(dev, M, bps, NKL):
+    """17-64 rows with each wave over several 16-column groups and one K
+    slice, the slices in separate workgroups: partials summed by the split-K
+    reduce in slice order, or with one slice the epilogue in the kernel;
+    preshuffled and row-major B."""
+    N, K, l2 = NKL
+    name = ("ga_mxfp8_bf16_BpreShuffle_256x256_splitK" if bps else
+            "ga_mxfp8_bf16_noBpreShuffle_128x128_splitK")
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=3 * M + l2, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    assert ld.gdz == 1 << l2
+    check(got, expect(qa, sa, qb, sb, l2), "decode split %s M=%d N=%d K=%d gdz=%d" %
+          ("bps" if bps else "plain", M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
+def test_decode_split_epilogue(dev):
+    """alpha/beta through the split variant (applied by the split-K reduce)."""
+    M, N, K, l2 = 40, 512, 2048, 2
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_256x256_splitK")
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=41)
+    rng = np.random.default_rng(41)
+    c_in = oracle.to_bf16_bits(rng.standard_normal((M, N)).astype(np.float32))
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2, alpha=0.5, beta=2.0, c_in=c_in)
+    assert ld.gdz == 4
+    acc = oracle.gemm_mx_mfma(qa, sa, qb, sb, l2, 1.0)
+    want_f = (np.float32(0.5) * acc).astype(np.float32) + np.float32(2.0) * \
+        oracle.bf16_bits_to_f32(c_in)
+    check(got, oracle.to_bf16_bits(want_f.astype(np.float32)), "decode split alpha/beta",
+          0.5 * oracle.mx_absdot(qa, sa, qb, sb))
+
+
 def _mx_device_problem(dev, M, N, K, cfg, l2, seed):
     qa, sa, qb, sb = mx_operands(M, N, K, seed=seed)
     sh = f4gemm.Shape(M, N, K)
@@ -324,16 +377,18 @@ def _mx_device_problem(dev, M, N, K, cfg, l2, seed):
     return (qa, sa, qb, sb), D, ld, args, keep
 
 
-@pytest.mark.parametrize("name", ["ga_mxfp8_bf16_BpreShuffle_256x256_splitK",
-                                  "ga_mxfp8_bf16_BpreShuffle_128x128_splitK",
-                                  "ga_mxfp8_bf16_BpreShuffle_64x256_splitK"])
-def test_ws_handle_graph_replay_survives_grow(dev, name):
+@pytest.mark.parametrize("name,M", [("ga_mxfp8_bf16_BpreShuffle_256x256_splitK", 256),
+                                    ("ga_mxfp8_bf16_BpreShuffle_128x128_splitK", 256),
+                                    ("ga_mxfp8_bf16_BpreShuffle_64x256_splitK", 256),
+                                    ("ga_mxfp8_bf16_BpreShuffle_256x256_splitK", 48)])
+def test_ws_handle_graph_replay_survives_grow(dev, name, M):
     """ga_kernel_launch_ws_handle: a split-K GEMM captured into a HIP graph
     with its workspace found through a device slot keeps giving the eager
     result after the slot's buffer is grown (and moved) between replays; a
-    slot never reserved is refused on the host."""
+    slot never reserved is refused on the host. M = 48 runs the decode
+    kernel's split variant (slices in separate workgroups)."""
     from gcnasm_amd import flatmm_splitk as fs
-    M, N, K, l2 = 256, 1024, 4096, 2
+    N, K, l2 = 1024, 4096, 2
     cfg = cfg_named(name)
     (qa, sa, qb, sb), D, ld, args, keep = _mx_device_problem(dev, M, N, K, cfg, l2, 21)
     assert ld.gdz == 4
@@ -348,7 +403,7 @@ def test_ws_handle_graph_replay_survives_grow(dev, name):
         kern.launch(args, ld.gdx, ld.gdy, ld.gdz, ws_handle=h)
         torch.cuda.synchronize()
         eager = D[:M].view(torch.int16).cpu().numpy().view(np.uint16).copy()
-        check(eager, expect(qa, sa, qb, sb, l2), "ws handle eager %s" % name,
+        check(eager, expect(qa, sa, qb, sb, l2), "ws handle eager %s M=%d" % (name, M),
               oracle.mx_absdot(qa, sa, qb, sb))
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())

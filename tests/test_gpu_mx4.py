@@ -230,6 +230,23 @@ def test_fp4_decode_plain_b(dev):
     check4(got, qa, sa, qb, sb, 0, "decode plain B")
 
 
+@pytest.mark.parametrize("M", [24, 64])
+@pytest.mark.parametrize("bps", [True, False])
+@pytest.mark.parametrize("NKL", [(1040, 4096, 2), (8192, 2048, 2), (19216, 512, 0),
+                                 (28672 - 16, 512, 0), (28672 - 16, 1024, 1),
+                                 (19216, 2048, 2)])
+def test_fp4_decode_split_across_workgroups(dev, M, bps, NKL):
+    """17-64 rows with each wave over several 16-column groups and one K
+    slice, slices in separate workgroups (partials summed by the split-K
+    reduce), or one slice with the epilogue in the kernel."""
+    N, K, l2 = NKL
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + 9)
+    name = ("ga_mxfp4_bf16_BpreShuffle_256x256_splitK" if bps else
+            "ga_mxfp4_bf16_noBpreShuffle_128x128_splitK")
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4(name), l2)
+    check4(got, qa, sa, qb, sb, l2, "decode split %s M=%d" % (name, M))
+
+
 def test_fp4_k_not_multiple_of_256_is_rejected(dev):
     M, N, K = 64, 256, 384
     sh = f4gemm.Shape(M, N, K, elem_bits=4)

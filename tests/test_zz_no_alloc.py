@@ -46,7 +46,11 @@ def _bits(D, M):
                                   "ga_mxfp8_bf16_BpreShuffle_64x256_splitK"])
 def test_noalloc_matches_workspace_launch(dev, name):
     lib = _lib.lib()
-    for (M, N, K, l2, seed) in ((512, 2048, 4096, 2, 1), (256, 1024, 2048, 1, 2)):
+    # the 256x256 kernel also at 17-64 rows (the decode kernel's split variant)
+    cases = [(512, 2048, 4096, 2, 1), (256, 1024, 2048, 1, 2)]
+    if name.endswith("256x256_splitK"):
+        cases += [(64, 4096, 8192, 3, 4), (40, 2064, 4096, 2, 5), (64, 28672, 1024, 1, 6)]
+    for (M, N, K, l2, seed) in cases:
         idx, ld, outs, bufs = _problem(dev, M, N, K, name, l2, seed)
         assert ld.gdz == 1 << l2
         (D0, a0), (D1, a1) = outs
