@@ -637,10 +637,11 @@ def main():
     # first, on an idle GPU: right after the MFMA-heavy legs the power
     # controller leaves the memory path a few percent slower for about a second.
     if "decode" in legs:
-        # each shape at the reference driver's default log2_k_split = 0 (the
-        # reported value) and, beside it, at the heuristic's own split
-        # (log2_k_split = -1; the configuration allows split-K, but on these
-        # shapes the split is slower)
+        # each shape at log2_k_split 0..3 (the configuration allows split-K;
+        # 0 is the reference driver's default): the reported value is the
+        # fastest split, named in the entry, with every split's figure and
+        # the split the heuristic (log2_k_split = -1) picks beside it. A split
+        # call's time covers both its kernels (K slices + split-K reduce).
         decode = []
         for dM, dN, dK in ((16, 28672, 8192), (16, 8192, 28672), (1, 28672, 8192),
                            (1, 8192, 28672), (64, 28672, 8192), (64, 8192, 28672)):
@@ -648,7 +649,7 @@ def main():
             dbytes = dM * dK + dN * dK + (dM + dN) * dK / 32 + 2 * dM * dN
             wl = "mxfp8_gemm_decode_%dx%dx%d" % (dM, dN, dK)
             res = {}
-            for l2 in (-1, 0):
+            for l2 in (0, 1, 2, 3):
                 dr = time_gemm(torch, f4gemm, da, dbs, dM, dN, dK, max(args.steps, 30),
                                args.warmup, log2_k_split=l2)
                 dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
@@ -657,11 +658,16 @@ def main():
                            "grid": [dr["ld"].gdx, dr["ld"].gdy, dr["ld"].gdz],
                            "kernel_avg_us": round(dr["avg_us"], 2),
                            "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4)}
+            best = max(res, key=lambda l: res[l]["value"])
+            _, heur = f4gemm.select_kernel(dM, dN, dK, 256, -1, 1)
             e = {"workload": wl}
-            e.update(res[0])
+            e.update(res[best])
             e.update({"algorithmic_bytes": int(dbytes), "weight_sets": 3,
-                      "roofline": roofline(wl, res[0]["value"], "hbm", HBM_PEAK_GBS, "GB/s"),
-                      "heuristic_split": res[-1]})
+                      "roofline": roofline(wl, res[best]["value"], "hbm", HBM_PEAK_GBS, "GB/s"),
+                      "heuristic_log2_k_split": heur,
+                      "by_log2_k_split": {str(l): {k: res[l][k] for k in
+                                                   ("value", "kernel_avg_us", "frac_hbm")}
+                                          for l in sorted(res)}})
             decode.append(e)
             del da, dbs
             torch.cuda.empty_cache()

@@ -13,16 +13,21 @@
 //    owns 64 rows (by group) x 32 columns (by SIMD): 4 x 2 MFMA tiles of
 //    16x16, 8 MFMAs of 16x16x128 per quadrant per K step, 128 accumulator
 //    VGPRs in all.
-//  * One K step (128) is four phases, one quadrant each (00, 01, 10, 11).
-//    Each phase reads ONE operand fragment (A rows of an M half, or B columns
-//    of an N half: A0, B1, A1, then B0 of the next step) and multiplies it
-//    with the fragment kept from the previous phase; the read overlaps the
-//    other group's MFMA slot.
+//  * One K step (128) is two parts per group, two quadrants each: X = 00 +
+//    01 (A rows of M half 0 with both B halves), Y = 10 + 11 (A half 1 with
+//    the same B fragments). Each part is a memory half (copies, then the LDS
+//    reads of the fragments the part multiplies: A0, B0 and B1 before X, A1
+//    before Y) and an MFMA half (16 MFMAs); a group's memory half overlaps
+//    the other group's MFMA half, so a SIMD's MFMA pipe changes waves twice
+//    per K step per group (measured on MI355X, MXFP8 8192^3: 458 -> 403 us
+//    against one quadrant per part).
 //  * LDS: A and B each hold two K-step slots of two 16 KB half tiles, plus a
 //    ring of three 4 KB scale slots: 140 KB. A half tile is refilled with the
-//    step two ahead once both groups have read it, so its copy has six phases
-//    to land; every phase ends with a counted vmcnt wait on the copy the next
-//    phase reads.
+//    step two ahead once both groups have read it (A1 one ahead); every
+//    half-part ends with the same counted wait, vmcnt(8 + scale copies per
+//    step) and lgkmcnt(0), then the workgroup barrier: the copies the next
+//    half-part reads have landed in every wave, and every LDS read issued
+//    before the barrier is complete before any copy issued after it.
 //  * A shuffled scale dword covers 256 K, a pair of K steps, so a ring slot
 //    holds one pair (8 A then 8 B 32-row blocks) and each step copies half of
 //    the pair two ahead: one 4-byte-per-lane copy per wave per step.
@@ -155,36 +160,11 @@ __device__ __forceinline__ uint32_t read_sb(const ReadBase& rb, int ring, uint32
         return *(const uint16_t*)p;
 }
 
-// One quadrant: 4 A tiles x 2 B tiles; the scale byte is 2*(128-K half) +
+// Quadrant MFMAs: 4 A tiles x 2 B tiles; the scale byte is 2*(128-K half) +
 // (16-row half inside the 32-row scale block). MXFP8: one MFMA per tile (the
 // step's 128 K; its half is in bytes 0-1 of the scale operands). MXFP4: the
 // fragment's first 16 bytes per lane are K [0, 128) of the 256-K step and
 // its last 16 bytes K [128, 256): two MFMAs per tile, halves 0 and 1.
-template <bool FP4>
-__device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], const v8i (&a)[4],
-                                             const v8i (&b)[2], const uint32_t (&sa)[2],
-                                             uint32_t sb)
-{
-    __builtin_amdgcn_s_setprio(1);
-    static_for<4>([&](auto I) {
-        constexpr int i = decltype(I)::value;
-        static_for<2>([&](auto T) {
-            constexpr int t = decltype(T)::value;
-            if constexpr (FP4) {
-                acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
-                                                            (int)sa[i >> 1]);
-                acc[i][t] = mfma_mx16_fp4<2 + (t & 1), 2 + (i & 1)>(hi16(b[t]), hi16(a[i]),
-                                                                    acc[i][t], (int)sb,
-                                                                    (int)sa[i >> 1]);
-            } else {
-                acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
-                                                        (int)sa[i >> 1]);
-            }
-        });
-    });
-    __builtin_amdgcn_s_setprio(0);
-}
-
 // The kernel-argument fields a tile uses (names as in ga_f4gemm_kargs), read
 // once at kernel entry and made wave-uniform: the compiler fetches this large
 // by-value argument with vector loads, and every address derived from a VGPR
@@ -210,6 +190,48 @@ struct PpArgs {
 // and K count elements. A K step is 256 elements = the same 128 bytes per row
 // as an MXFP8 step, so copies, LDS layout and fragment reads are shared; a
 // step reads one whole shuffled scale dword per 32-row block.
+// Two quadrants with shared A fragments: acc0 += A x B0, acc1 += A x B1
+// (16 MFMAs at raised issue priority).
+template <bool FP4>
+__device__ __forceinline__ void mma_two(v4f (&acc0)[4][2], v4f (&acc1)[4][2], const v8i (&a)[4],
+                                        const v8i (&b0)[2], const v8i (&b1)[2],
+                                        const uint32_t (&sa)[2], uint32_t sb0, uint32_t sb1)
+{
+    __builtin_amdgcn_s_setprio(1);
+    auto quadrant = [&](v4f (&acc)[4][2], const v8i (&b)[2], uint32_t sb) {
+        static_for<4>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            static_for<2>([&](auto T) {
+                constexpr int t = decltype(T)::value;
+                if constexpr (FP4) {
+                    acc[i][t] = mfma_mx16_fp4<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+                                                                (int)sa[i >> 1]);
+                    acc[i][t] = mfma_mx16_fp4<2 + (t & 1), 2 + (i & 1)>(
+                        hi16(b[t]), hi16(a[i]), acc[i][t], (int)sb, (int)sa[i >> 1]);
+                } else {
+                    acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
+                                                            (int)sa[i >> 1]);
+                }
+            });
+        });
+    };
+    quadrant(acc0, b0, sb0);
+    quadrant(acc1, b1, sb1);
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// Half-part boundary: own copies older than the last N landed, own LDS reads
+// complete, then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void part_sync()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<N>();
+    wait_lgkmcnt0();
+    wait_lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <bool BPS, bool FP4>
 __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ ws,
                                         char* smem, int tile_m, int tile_n)
@@ -309,106 +331,88 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
         uint32_t sa[2], sb0, sb1;
 
         // Prologue: the copies a steady pipeline would have issued before
-        // step 0, in the same order, then the read of the phase before step 0
-        // (B0). MXFP8: scales of pair 0; B0 + A scales of pair 1, A0, B1, A1
-        // of step 0; B0 + B scales of pair 1, A0, B1 of step 1. MXFP4: B0 +
-        // scales, A0, B1, A1 of step 0; B0 + scales, A0, B1 of step 1.
-        if constexpr (FP4) {
-            issue_b(L, smem, 0, 0, wave);
+        // step 0, in the same order (Y of steps -2 and -1, X of step -1),
+        // MXFP8 preceded by both halves of the scales of pair 0: A0, B0, B1
+        // + scales of step 0 (MXFP8: half 0 of pair 1), A1 of step 0, A0,
+        // B0, B1 + scales of step 1 (MXFP8: half 1 of pair 1).
+        constexpr int kS = FP4 ? 2 : 1; // scale copies per step
+        if constexpr (!FP4) {
             issue_s(L, smem, 0, 0, 0, wave);
             issue_s(L, smem, 0, 1, 0, wave);
-            issue_a(L, smem, 0, 0, wave);
-            issue_b(L, smem, 1, 0, wave);
-            issue_a(L, smem, 1, 0, wave);
-            issue_b(L, smem, 0, 1, wave);
-            issue_s(L, smem, 1, 0, 1, wave);
-            issue_s(L, smem, 1, 1, 1, wave);
-            issue_a(L, smem, 0, 1, wave);
-            issue_b(L, smem, 1, 1, wave);
-            phase_sync<16>(); // B0 of step 0
-            read_b<0>(rb, 0, fb0);
-            phase_sync<12>(); // A0 and the scales of step 0
-        } else {
-            issue_s(L, smem, 0, 0, 0, wave);
-            issue_s(L, smem, 0, 1, 0, wave);
-            issue_b(L, smem, 0, 0, wave);
-            issue_s(L, smem, 1, 0, 1, wave);
-            issue_a(L, smem, 0, 0, wave);
-            issue_b(L, smem, 1, 0, wave);
-            issue_a(L, smem, 1, 0, wave);
-            issue_b(L, smem, 0, 1, wave);
-            issue_s(L, smem, 1, 1, 1, wave);
-            issue_a(L, smem, 0, 1, wave);
-            issue_b(L, smem, 1, 1, wave);
-            phase_sync<14>(); // B0 of step 0 and the scales of pair 0
-            read_b<0>(rb, 0, fb0);
-            phase_sync<11>(); // A0 of step 0
         }
-        // Retire pending scalar loads (epilogue arguments) here: with one in
-        // flight the compiler cannot count LDS reads inside the loop and
-        // falls back to full waits.
-        wait_lgkmcnt0();
+        issue_a(L, smem, 0, 0, wave);
+        issue_b(L, smem, 0, 0, wave);
+        issue_b(L, smem, 1, 0, wave);
+        if constexpr (FP4) {
+            issue_s(L, smem, 0, 0, 0, wave);
+            issue_s(L, smem, 0, 1, 0, wave);
+        } else {
+            issue_s(L, smem, 1, 0, 1, wave);
+        }
+        issue_a(L, smem, 1, 0, wave);
+        issue_a(L, smem, 0, 1, wave);
+        issue_b(L, smem, 0, 1, wave);
+        issue_b(L, smem, 1, 1, wave);
+        if constexpr (FP4) {
+            issue_s(L, smem, 1, 0, 1, wave);
+            issue_s(L, smem, 1, 1, 1, wave);
+        } else {
+            issue_s(L, smem, 1, 1, 1, wave);
+        }
+        // (also retires pending scalar loads: with one in flight the
+        // compiler cannot count LDS reads inside the loop)
+        part_sync<8 + kS>();
         if (grp == 1)
             slot_sync(); // second group runs one barrier behind
 
-        // One K step s of parity P (LDS slot P). A memory slot issues its
-        // copy (a half tile two steps ahead, into a half both groups have
-        // finished reading) before its LDS reads, then waits for the copy
-        // the next phase reads:
-        //   phase  read        copy           quadrant   younger copies
-        //   1      A0(s)       A1(s+1)        00         11
-        //   2      B1(s)       B0(s+2), S     01         12
-        //   3      A1(s)       A0(s+2)        10         12
-        //   4      B0(s+1)     B1(s+2)        11         11
-        // MXFP8: S is half P of the scales of pair (s >> 1) + 2 (ring slot
-        // r2, the slot of pair (s >> 1) - 1, whose last read was in step s - 1
-        // or earlier); the scales a phase reads were copied at least two steps
-        // before the operand copy it waits for, so that wait covers them.
-        // MXFP4: S is both halves of the scales of step s + 2 (2 copies, ring
-        // slot (s + 2) % 3 = the slot of step s - 1); they are read from
-        // phase 1 of step s + 2, after the wait for A0(s + 2), which was
-        // issued after them. Younger copies per phase: 12, 14, 14, 12.
-        constexpr int kS = FP4 ? 2 : 1;
+        // Step s of parity P (LDS slot P), per group:
+        //   X memory: copy A1(s+1) (2 per wave); read the scales, A0(s),
+        //             B0(s), B1(s)
+        //   X MFMA:   quadrants 00, 01
+        //   Y memory: copy A0(s+2), B0(s+2), B1(s+2) (6) and the scales S;
+        //             read A1(s)
+        //   Y MFMA:   quadrants 10, 11
+        // A copy writes a slot both groups last read at least one barrier
+        // earlier (reads complete at every barrier). Every half-part ends
+        // with vmcnt(8 + kS): after X memory that retires X(s-1), i.e.
+        // A1(s), read in Y; after Y memory, Y(s-1): A0, B0, B1 of step s+1
+        // and (copied at least as early) its scales, read in X of step s+1.
+        // MXFP8: S is half P of the scales of pair (s >> 1) + 2, into ring
+        // slot r2 (that of pair (s >> 1) - 1, last read in step s - 1);
+        // MXFP4: both halves of the scales of step s + 2, into ring slot
+        // (s + 2) % 3 (that of step s - 1).
         int r0 = 0; // scale ring slot of step s (MXFP8: of pair s >> 1)
         for (int s = 0; s < nsteps; s++) {
             const int P = s & 1;
             const uint32_t hb = FP4 ? 0u : (uint32_t)P * 2;
             const int r1 = (FP4 || P) ? (r0 == 2 ? 0 : r0 + 1) : r0; // slot of step s + 1
             const int r2 = r0 == 0 ? 2 : r0 - 1;                       // (r0 + 2) % 3
-            // phase 1
+            // X
             issue_a(L, smem, 1, s + 1, wave);
             read_sa<0, FP4>(rb, r0, hb, sa);
             sb0 = read_sb<0, FP4>(rb, r0, hb);
+            sb1 = read_sb<1, FP4>(rb, r0, hb);
             read_a<0>(rb, P, fa);
-            phase_sync<10 + kS>();
-            mma_quadrant<FP4>(acc[0], fa, fb0, sa, sb0);
-            slot_sync();
-            // phase 2
+            read_b<0>(rb, P, fb0);
+            read_b<1>(rb, P, fb1);
+            part_sync<8 + kS>();
+            mma_two<FP4>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
+            part_sync<8 + kS>();
+            // Y
+            issue_a(L, smem, 0, s + 2, wave);
             issue_b(L, smem, 0, s + 2, wave);
+            issue_b(L, smem, 1, s + 2, wave);
             if constexpr (FP4) {
                 issue_s(L, smem, s + 2, 0, r2, wave);
                 issue_s(L, smem, s + 2, 1, r2, wave);
             } else {
                 issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
             }
-            sb1 = read_sb<1, FP4>(rb, r0, hb);
-            read_b<1>(rb, P, fb1);
-            phase_sync<10 + 2 * kS>();
-            mma_quadrant<FP4>(acc[1], fa, fb1, sa, sb1);
-            slot_sync();
-            // phase 3
-            issue_a(L, smem, 0, s + 2, wave);
             read_sa<1, FP4>(rb, r0, hb, sa);
             read_a<1>(rb, P, fa);
-            phase_sync<10 + 2 * kS>();
-            mma_quadrant<FP4>(acc[2], fa, fb0, sa, sb0);
-            slot_sync();
-            // phase 4
-            issue_b(L, smem, 1, s + 2, wave);
-            read_b<0>(rb, P ^ 1, fb0);
-            phase_sync<10 + kS>();
-            mma_quadrant<FP4>(acc[3], fa, fb1, sa, sb1);
-            slot_sync();
+            part_sync<8 + kS>();
+            mma_two<FP4>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
+            part_sync<8 + kS>();
             r0 = r1;
         }
         if (grp == 0)
