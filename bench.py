@@ -68,6 +68,12 @@ def parse():
     ap.add_argument("--legs", default="all",
                     help="comma-separated subset of: " + ",".join(LEGS) + " (default all; "
                          "one leg at a time attributes rocprofv3 counters to one workload)")
+    ap.add_argument("--profile-workload", default=None, metavar="NAME",
+                    help="counter run: the calibration copies, then --steps calls of one "
+                         "workload (" + ", ".join(PROFILE_WORKLOADS) + "), nothing else timed")
+    ap.add_argument("--traffic-summary", default=None, metavar="DIR",
+                    help="write profiles/traffic.json from the rocprofv3 counter runs under "
+                         "DIR/<workload>/{FETCH_SIZE,WRITE_SIZE}/")
     return ap.parse_args()
 
 
@@ -488,11 +494,149 @@ def deepseek_legs(torch, ops, opus_gemm, steps, warmup):
     return out
 
 
-def measured_traffic(workload, kernel=None):
+# Workloads a counter run can isolate: name -> (kind, M, N, K, log2_k_split).
+# The decode entries carry the split the decode leg reports for the shape.
+PROFILE_WORKLOADS = {
+    "mxfp8_gemm_8192x8192x8192": ("mx", 8192, 8192, 8192, 0),
+    "mxfp8_gemm_4096x4096x4096": ("mx", 4096, 4096, 4096, 0),
+    "mxfp8_gemm_decode_16x28672x8192": ("mxd", 16, 28672, 8192, 0),
+    "mxfp8_gemm_decode_16x8192x28672": ("mxd", 16, 8192, 28672, 0),
+    "mxfp8_gemm_decode_1x28672x8192": ("mxd", 1, 28672, 8192, 0),
+    "mxfp8_gemm_decode_1x8192x28672": ("mxd", 1, 8192, 28672, 0),
+    "mxfp8_gemm_decode_64x28672x8192": ("mxd", 64, 28672, 8192, 1),
+    "mxfp8_gemm_decode_64x8192x28672": ("mxd", 64, 8192, 28672, 2),
+    "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out": ("bs", 8192, 8192, 8192, 0),
+    "fp8_per_tensor_8192x8192x8192_bf16out": ("pt", 8192, 8192, 8192, 0),
+    "fp8_blockscale_deepseek_4096x7168x2048": ("bs", 4096, 7168, 2048, 0),
+    "fp8_blockscale_deepseek_4096x2112x7168": ("bs", 4096, 2112, 7168, 0),
+    "fp8_blockscale_deepseek_4096x24576x1536": ("bs", 4096, 24576, 1536, 0),
+    "mxfp4_gemm_8192x8192x8192": ("mx4", 8192, 8192, 8192, 0),
+}
+
+# Library kernels a workload's calls launch (the GEMM and, for split-K, the
+# reduce); the quantisers and torch's set-up kernels are not part of a call.
+def _call_kernel(name):
+    return name.startswith("void ga::") and "quant" not in name
+
+
+def _mx_choice(f4gemm, M, N, K, l2, eb):
+    """The manifest kernel and split time_gemm runs for a shape (the heuristic's
+    choice for the given log2_k_split)."""
+    table = f4gemm.manifest() if eb == 8 else f4gemm.manifest_fp4()
+    idx, l2 = f4gemm.select_kernel(M, N, K, 256, l2, 1, cfgs=None if eb == 8 else table)
+    return table[idx], l2
+
+
+def profile_workload(torch, name, calls):
+    """Sets up one workload, then runs `calls` calls of it back to back (the
+    counter run's dispatches after the set-up are exactly those calls)."""
+    from gcnasm_amd import f4gemm, opus_gemm, ops
+    kind, M, N, K, l2 = PROFILE_WORKLOADS[name]
+    if kind in ("mx", "mxd", "mx4"):
+        eb = 4 if kind == "mx4" else 8
+        a, bs = mx_problem(torch, ops, f4gemm, M, N, K, b_std=0.02 if kind == "mxd" else 1.0,
+                           nsets=3 if kind == "mxd" else 1, seed=1, elem_bits=eb)
+        sh = f4gemm.Shape(M, N, K, elem_bits=eb)
+        cfg, l2 = _mx_choice(f4gemm, M, N, K, l2, eb)
+        ld = f4gemm.make_launch(cfg, M, N, K, l2)
+        kern = f4gemm.Kernel().load(None, cfg)
+        D = torch.empty((sh.d_rows_pad(), N), dtype=torch.bfloat16, device="cuda:0")
+        ws = torch.empty(max(1, ld.gdz * M * N), dtype=torch.float32, device="cuda:0")
+        args = [f4gemm.fill_args(D, None, a.codes, b.codes, a.scales, b.scales, M, N, K, N,
+                                 sh.scale_cols(), sh.scale_cols(), 1.0, 0.0, ld.log2_k_split)
+                for b in bs]
+        torch.cuda.synchronize()
+        for i in range(calls):
+            kern.launch(args[i % len(args)], ld.gdx, ld.gdy, ld.gdz, workspace=ws)
+        info = {"kernel": cfg.knl_name, "log2_k_split": ld.log2_k_split}
+    else:
+        xa, xb = scaled_inputs(torch, M, N, K, seed=17)
+        if kind == "pt":
+            qa, sa = ops.quant_fp8_per_tensor(xa)
+            qb, sb = ops.quant_fp8_per_tensor(xb)
+            c, gn = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0"), 0
+        else:
+            qa, sa = ops.quant_fp8_1x128(xa)
+            qb, sb = ops.quant_fp8_128x128(xb)
+            c, gn = torch.empty((M, N), dtype=torch.float32, device="cuda:0"), 128
+        del xa, xb
+        ka = opus_gemm.make_kargs(qa, qb, c, sa, sb, M, N, K, 1, gn)
+        out = opus_gemm._out_dtype(c)
+        torch.cuda.synchronize()
+        for _ in range(calls):
+            if gn == 0:
+                opus_gemm.fp8_gemm(ka, out)
+            else:
+                opus_gemm.gemm_a8w8_blockscale(ka, out, gn)
+        info = {"kernel": "fp8_gemm" if gn == 0 else "gemm_a8w8_blockscale", "log2_k_split": 0}
+    torch.cuda.synchronize()
+    return info
+
+
+def traffic_summary(root_dir, calls):
+    """profiles/traffic.json from counter runs of `bench.py --calib-copy
+    --profile-workload W --steps calls` (FETCH_SIZE, then WRITE_SIZE, in KiB
+    per dispatch). Each counter is scaled by what it reads for the 512 MiB
+    device copy (the first two dispatches); a call's traffic is the sum over
+    the workload's library dispatches divided by the number of calls."""
+    import csv
+    res = {}
+    for wl in sorted(os.listdir(root_dir)):
+        if wl not in PROFILE_WORKLOADS:
+            continue
+        per = {}
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            rows = []
+            for dp, _, files in os.walk(os.path.join(root_dir, wl, ctr)):
+                for f in files:
+                    if f.endswith("counter_collection.csv"):
+                        with open(os.path.join(dp, f)) as fh:
+                            rows += list(csv.DictReader(fh))
+            byd = {}
+            for r in rows:
+                if r["Counter_Name"] != ctr:
+                    continue
+                d = byd.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], 0.0])
+                d[1] += float(r["Counter_Value"])
+            seq = [byd[k] for k in sorted(byd)]
+            copies = [v for n, v in seq if "copyBuffer" in n][:2]
+            calls_kib = [v for n, v in seq if _call_kernel(n)]
+            if len(copies) < 2 or not calls_kib:
+                break
+            factor = (512 * 1024.0) / (sum(copies) / len(copies))
+            per[ctr] = {"bytes_per_call": sum(calls_kib) * 1024.0 * factor / calls,
+                        "factor": round(factor, 4), "dispatches": len(calls_kib)}
+        if len(per) == 2:
+            kind, M, N, K, l2 = PROFILE_WORKLOADS[wl]
+            kernel = None
+            if kind in ("mx", "mxd", "mx4"):
+                from gcnasm_amd import f4gemm
+                kernel = _mx_choice(f4gemm, M, N, K, l2, 4 if kind == "mx4" else 8)[0].knl_name
+            res[wl] = {"kernel": kernel,
+                       "bytes_per_launch": int(per["FETCH_SIZE"]["bytes_per_call"] +
+                                               per["WRITE_SIZE"]["bytes_per_call"]),
+                       "fetch_bytes": int(per["FETCH_SIZE"]["bytes_per_call"]),
+                       "write_bytes": int(per["WRITE_SIZE"]["bytes_per_call"]),
+                       "fetch_factor": per["FETCH_SIZE"]["factor"],
+                       "write_factor": per["WRITE_SIZE"]["factor"],
+                       "log2_k_split": l2, "calls": calls,
+                       "command": "rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} --output-format csv "
+                                  "-- python3 bench.py --calib-copy --profile-workload %s "
+                                  "--steps %d" % (wl, calls)}
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    with open(path, "w") as f:
+        json.dump({"note": "HBM bytes per call from FETCH_SIZE + WRITE_SIZE, each scaled by its "
+                           "reading for a 512 MiB device copy; a split-K call counts its "
+                           "reduce", "workloads": res}, f, indent=1, sort_keys=True)
+    return path
+
+
+def measured_traffic(workload, kernel=None, log2_k_split=None):
     """HBM bytes per launch of a workload's kernel from the committed
     rocprofv3 counter summary (profiles/traffic.json: FETCH_SIZE +
     WRITE_SIZE per dispatch, each calibrated on a 512 MiB device copy), or
-    None when none is committed for it (or it was measured on another kernel)."""
+    None when none is committed for it (or it was measured on another kernel
+    or split)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -501,12 +645,15 @@ def measured_traffic(workload, kernel=None):
         return None
     if kernel is not None and t.get("kernel") not in (None, kernel):
         return None
+    if log2_k_split is not None and t.get("log2_k_split") not in (None, log2_k_split):
+        return None
     return t.get("bytes_per_launch")
 
 
-def roofline(workload, achieved, bound, peak, unit, kernel=None):
+def roofline(workload, achieved, bound, peak, unit, kernel=None, log2_k_split=None):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, kernel)}
+            "frac": round(achieved / peak, 4),
+            "traffic": measured_traffic(workload, kernel, log2_k_split)}
 
 
 def cpu_info():
@@ -609,6 +756,9 @@ def cpu_legs():
 
 def main():
     args = parse()
+    if args.traffic_summary:
+        print(traffic_summary(args.traffic_summary, args.steps))
+        return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (--gpus %d requested); the sharded "
               "design is described in DESIGN.md" % args.gpus, file=sys.stderr)
@@ -630,6 +780,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.profile_workload:
+        if args.profile_workload not in PROFILE_WORKLOADS:
+            print("bench.py: unknown workload %s" % args.profile_workload, file=sys.stderr)
+            sys.exit(2)
+        info = profile_workload(torch, args.profile_workload, args.steps)
+        print(json.dumps({"profile_workload": args.profile_workload, "calls": args.steps,
+                          **info}), flush=True)
+        return
 
     extra = {}
     # decode: HBM-bound; rotate weight sets so the Infinity Cache cannot
@@ -663,7 +822,8 @@ def main():
             e = {"workload": wl}
             e.update(res[best])
             e.update({"algorithmic_bytes": int(dbytes), "weight_sets": 3,
-                      "roofline": roofline(wl, res[best]["value"], "hbm", HBM_PEAK_GBS, "GB/s"),
+                      "roofline": roofline(wl, res[best]["value"], "hbm", HBM_PEAK_GBS, "GB/s",
+                                           log2_k_split=res[best]["log2_k_split"]),
                       "heuristic_log2_k_split": heur,
                       "by_log2_k_split": {str(l): {k: res[l][k] for k in
                                                    ("value", "kernel_avg_us", "frac_hbm")}
