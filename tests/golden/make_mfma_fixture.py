@@ -2,6 +2,7 @@
 
     python tests/golden/make_mfma_fixture.py build          # here: hipcc the probe
     python tests/golden/make_mfma_fixture.py run OUT.npz    # on an MI355X
+    python tests/golden/make_mfma_fixture.py run-f8 OUT.npz # E4M3 / E5M2 pairs
 
 `build` compiles mfma_probe.hip (one v_mfma_scale_f32_16x16x128_f8f6f4 per
 wave) into tests/golden/libmfma_probe.so; `run` feeds it the seeded cases
@@ -10,6 +11,10 @@ order), SA, SB [case, 16, 4] E8M0 codes (one per row and 32-K block), C and
 the hardware's D [case, 16, 16] fp32 (D[i][j] = C[i][j] + sum_k A[i,k] B[j,k]
 scaled) and a tag per case. The committed fixture mfma_fp8_hw.npz pins the
 oracle's model of the instruction's step sum (tests/test_oracle_mfma.py).
+
+`run-f8` records every pairing of E4M3 and E5M2 operands (mfma_f8_hw.npz,
+FA / FB: the format codes) on f8_cases, for the oracle's model of the E5M2
+and mixed-format step sums.
 
 Case kinds: "mx" (MX-quantised N(0,1) * 2^U[-4,4] rows with their E8M0
 scales, as the GEMMs see them), "pt" (per-tensor-quantised N(0,1) rows, unit
@@ -130,6 +135,98 @@ def cases(seed=2024):
     return out
 
 
+def f8_cases(fa, fb, seed):
+    """Cases for operand formats fa (A) and fb (B), 0 E4M3, 1 E5M2: MX-quantised
+    rows of each format, codes of every finite exponent, subnormal-heavy rows
+    and a cancelling mix (positive and negative products of close size)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    unit = np.full((16, 4), 127, np.uint8)
+    tables = {0: oracle.e4m3_decode_table().astype(np.float64),
+              1: oracle.e5m2_decode_table().astype(np.float64)}
+
+    def add(A, B, SA, SB, C, tag):
+        out.append((A.astype(np.uint8), B.astype(np.uint8), SA.astype(np.uint8),
+                    SB.astype(np.uint8), C.astype(np.float32), tag))
+
+    def c_like(A, B, SA, SB, zero):
+        if zero:
+            return np.zeros((16, 16))
+        va = tables[fa][A] * np.exp2(np.repeat(SA.astype(np.int64) - 127, 32, axis=1))
+        vb = tables[fb][B] * np.exp2(np.repeat(SB.astype(np.int64) - 127, 32, axis=1))
+        mag = np.median(np.abs(va @ vb.T)) + 1e-30
+        return rng.standard_normal((16, 16)) * mag * 4
+
+    def finite_codes(fmt, sub_frac=0.0):
+        c = rng.integers(0, 256, (16, 128)).astype(np.uint8)
+        if fmt == 1:  # exponent 31: inf / NaN
+            c = np.where(((c >> 2) & 31) == 31, c ^ 0x04, c)
+        else:         # 0x7F / 0xFF: NaN
+            c = np.where((c & 0x7F) == 0x7F, c ^ 1, c)
+        if sub_frac > 0:
+            m = rng.random((16, 128)) < sub_frac
+            sub = (rng.integers(0, 4 if fmt == 1 else 8, (16, 128)) |
+                   (rng.integers(0, 2, (16, 128)) << 7)).astype(np.uint8)
+            c = np.where(m, sub, c)
+        return c
+
+    for i in range(16):
+        xa = oracle.gen_mx_input(16, 128, 9000 + 2 * i, 1.0, 4)
+        xb = oracle.gen_mx_input(16, 128, 9001 + 2 * i, 1.0 if i % 2 else 0.02, 4)
+        qa, sa = oracle.quant_mx8(xa, fa)
+        qb, sb = oracle.quant_mx8(xb, fb)
+        add(qa, qb, sa, sb, c_like(qa, qb, sa, sb, i < 8), "mx")
+    for i in range(12):
+        qa, qb = finite_codes(fa), finite_codes(fb)
+        add(qa, qb, unit, unit, c_like(qa, qb, unit, unit, i < 6), "wide")
+    for i in range(6):
+        qa, qb = finite_codes(fa, 0.7), finite_codes(fb, 0.3)
+        add(qa, qb, unit, unit, c_like(qa, qb, unit, unit, i < 3), "sub")
+    for i in range(6):
+        # every product of a group within a few binades: sums that cancel
+        xa = rng.standard_normal((16, 128)).astype(np.float32)
+        xb = (np.sign(rng.standard_normal((16, 128))) *
+              np.exp2(rng.integers(-2, 3, (16, 128)))).astype(np.float32)
+        qa = oracle.e5m2_encode(xa) if fa else oracle.e4m3_encode(xa)
+        qb = oracle.e5m2_encode(xb) if fb else oracle.e4m3_encode(xb)
+        add(qa, qb, unit, unit, c_like(qa, qb, unit, unit, i < 3), "cancel")
+    return out
+
+
+def run_f8(path):
+    """Records every format pair (fa, fb) in {0, 1}^2 with f8_cases."""
+    lib = ctypes.CDLL(LIB)
+    P = lambda x: x.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    rec = {k: [] for k in ("A", "B", "SA", "SB", "C", "D", "tags", "FA", "FB")}
+    for fa in (0, 1):
+        for fb in (0, 1):
+            cs = f8_cases(fa, fb, 3100 + 2 * fa + fb)
+            E = len(cs)
+            a = np.ascontiguousarray(np.stack([pack_ab(c[0]) for c in cs]))
+            b = np.ascontiguousarray(np.stack([pack_ab(c[1]) for c in cs]))
+            sa = np.ascontiguousarray(np.stack([pack_s(c[2]) for c in cs]))
+            sb = np.ascontiguousarray(np.stack([pack_s(c[3]) for c in cs]))
+            c = np.ascontiguousarray(np.stack([pack_c(c[4]) for c in cs]))
+            d = np.zeros((E, 64, 4), np.float32)
+            print("mfma probe: formats %d x %d, %d cases" % (fa, fb, E), flush=True)
+            rc = lib.mfma_probe_run_fmt(P(a), P(b), P(c), P(sa), P(sb), P(d), E, fa, fb)
+            if rc != 0:
+                raise SystemExit("mfma_probe_run_fmt failed: hipError %d" % rc)
+            for i, x in enumerate(cs):
+                rec["A"].append(x[0])
+                rec["B"].append(x[1])
+                rec["SA"].append(x[2])
+                rec["SB"].append(x[3])
+                rec["C"].append(x[4])
+                rec["D"].append(unpack_d(d[i]))
+                rec["tags"].append(x[5])
+                rec["FA"].append(fa)
+                rec["FB"].append(fb)
+    np.savez_compressed(path, **{k: np.array(v) if k in ("tags", "FA", "FB") else np.stack(v)
+                                 for k, v in rec.items()})
+    print("wrote", path, flush=True)
+
+
 def build():
     subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O2", "-fPIC", "-shared",
                     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -165,5 +262,7 @@ if __name__ == "__main__":
         build()
     elif len(sys.argv) > 2 and sys.argv[1] == "run":
         run(sys.argv[2])
+    elif len(sys.argv) > 2 and sys.argv[1] == "run-f8":
+        run_f8(sys.argv[2])
     else:
         raise SystemExit(__doc__)

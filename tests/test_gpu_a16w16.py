@@ -194,7 +194,13 @@ def test_library_slot_equals_caller_slot(dev, shape):
     torch.cuda.synchronize()
     want = host_bits(c_ref)
     assert not np.any(np.isnan(oracle.bf16_bits_to_f32(want)))
-    # library slot, repeated launches
+    # the caller-slot result against the oracle (partials, then reduce with bias)
+    ws_o = oracle.a16w16_splitk_ws(ab, bb, split_k)
+    expect = oracle.splitk_reduce(ws_o[:, None], oracle.bf16_bits_to_f32(bf16_bits((N,), 5)))[0]
+    ok, st = bf16_compare(want, oracle.to_bf16_bits(expect),
+                          slice_absdot(ab, bb, split_k).sum(0), bound=BF16_MFMA_BOUND)
+    assert_parity(st, "  a16w16 caller slot", cap_frac=1.0)
+    # library slot, repeated launches: bit-identical to the caller slot
     c = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     with fs.WorkspaceHandle() as h:
         kf = fs.make_kargs(a, b, c, split_k, h, bias)

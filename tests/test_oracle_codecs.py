@@ -9,7 +9,10 @@
                compiled from asm_f4gemm/f4gemm_ref.hpp) and torch.float8_e8m0fnu
   bf16 RNE     vs torch .to(bfloat16) on random bit patterns and edge values
   FP4 LUT      vs the reference's kFp4Lut
-  MX scale     closed-form bracket of amax / 2^e for each rule
+  MX scale     closed-form bracket of amax / 2^e for each rule (E4M3 and E5M2 maxima)
+  E5M2 decode  all 256 codes vs torch.float8_e5m2; encode vs torch's conversion
+               after a clamp to +-57344 over every bf16 value up to 2^17, all ties
+               and random float32 bit patterns; finite-code round trip
 """
 import math
 
@@ -166,3 +169,72 @@ def test_floor_log2_exact():
     for a in amax_samples()[:5000]:
         assert O.or_floor_log2(float(a)) == math.floor(math.log2(float(a))) or \
             2.0 ** O.or_floor_log2(float(a)) <= float(a) < 2.0 ** (O.or_floor_log2(float(a)) + 1)
+
+
+# E5M2 (OCP bf8, the f8f6f4 format code 1 of the scaled MFMA, opus.hpp:1785)
+
+def e5m2_encode_inputs():
+    # every bf16 value with |x| <= 2^17 (all E5M2 binades, subnormals and past the maximum)
+    b = np.arange(0, 0x10000, dtype=np.uint32) << 16
+    x = f32(b)
+    x = x[np.isfinite(x) & (np.abs(x) <= 2.0 ** 17)]
+    t = oracle.e5m2_decode_table()
+    pos = np.sort(t[np.isfinite(t) & (t > 0)]).astype(np.float32)
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    near = np.concatenate([np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9))])
+    rng = np.random.default_rng(5)
+    rnd = f32(rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32))
+    rnd = rnd[np.isfinite(rnd)]
+    extra = np.array([0.0, -0.0, 57344.0, 61439.0, 61440.0, 1e30, -1e30, np.inf, -np.inf,
+                      2.0 ** -16, 1.5 * 2.0 ** -16, 2.0 ** -17, 2.0 ** -14, 1.125, 1.375],
+                     np.float32)
+    return np.concatenate([x, -x, mids, -mids, near, -near, rnd, extra]).astype(np.float32)
+
+
+def test_e5m2_decode_table_vs_torch():
+    ours = oracle.e5m2_decode_table()
+    ref = torch.arange(256, dtype=torch.uint8).view(torch.float8_e5m2).float().numpy()
+    for c in range(256):
+        if np.isnan(ref[c]):
+            assert np.isnan(ours[c]), c
+        else:
+            assert ours[c] == ref[c], (c, ours[c], ref[c])
+    assert ours[0x7B] == 57344.0 and ours[0x01] == 2.0 ** -16 and np.isinf(ours[0x7C])
+
+
+def test_e5m2_encode_vs_torch():
+    """Round to nearest even with saturation at +-57344 (torch's conversion
+    after a clamp), NaN -> 0x7F."""
+    x = e5m2_encode_inputs()
+    ours = oracle.e5m2_encode(x)
+    ref = torch.from_numpy(np.clip(x, -57344.0, 57344.0)).to(torch.float8_e5m2)
+    ref = ref.view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ours, ref)
+    assert oracle.e5m2_encode(np.array([np.nan], np.float32))[0] == 0x7F
+
+
+def test_e5m2_round_trip_all_finite_codes():
+    t = oracle.e5m2_decode_table()
+    codes = np.array([c for c in range(256) if np.isfinite(t[c])], np.uint8)
+    back = oracle.e5m2_encode(t[codes])
+    # -0 and +0 keep their sign; every finite code maps to itself
+    np.testing.assert_array_equal(back, codes)
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_mx_scale_rule_brackets_e5m2(rule):
+    """The E5M2 rules are the E4M3 ones with the format maximum 57344 =
+    1.75 * 2^15 in place of 448 = 1.75 * 2^8 (OCP emax 15 for rule 2)."""
+    O = oracle.load()
+    for a in amax_samples():
+        e = O.or_mx8_scale_exp(float(a), rule, 1)
+        if e in (-127, 127):
+            continue
+        a64 = float(a)
+        if rule == 0:
+            assert 57344.0 * 2.0 ** e <= a64 < 57344.0 * 2.0 ** (e + 1), (a64, e)
+        elif rule == 1:
+            assert 57344.0 * 2.0 ** (e - 1) < a64 <= 57344.0 * 2.0 ** e, (a64, e)
+        else:
+            assert 2.0 ** (e + 15) <= a64 < 2.0 ** (e + 16), (a64, e)
+        assert O.or_mx8_scale_exp(float(a), rule, 0) == O.or_mx_scale_exp(float(a), rule)

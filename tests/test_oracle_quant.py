@@ -128,3 +128,49 @@ def test_quant_per_tensor():
     np.testing.assert_array_equal(q.ravel(), nearest_codes((x / want).astype(np.float32)))
     q0, s0 = oracle.quant_fp8_per_tensor(np.zeros((4, 4), np.float32))
     assert s0[0] == 1.0 and not q0.any()
+
+
+def nearest_codes_e5m2(v):
+    """Brute-force RNE-saturating E5M2 code of each float32 value in v."""
+    t = oracle.e5m2_decode_table().astype(np.float64)
+    codes = np.array([c for c in range(256) if np.isfinite(t[c]) and c != 0x80])
+    vals = t[codes]
+    v = np.clip(np.asarray(v, np.float64).ravel(), -57344.0, 57344.0)
+    d = np.abs(v[:, None] - vals[None, :])
+    best = d.min(1, keepdims=True)
+    cand = d == best
+    pick = np.where(cand & ((codes[None, :] & 1) == 0), 1, 0) + cand
+    out = codes[np.argmax(pick, axis=1)]
+    neg0 = (t[out] == 0) & (np.signbit(np.asarray(v)))
+    return np.where(neg0, 0x80, out).astype(np.uint8)
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+def test_mx_quant_e5m2_brute_force(rule):
+    """MX 1x32 with E5M2 elements: scales by the E5M2 rule (format maximum
+    57344), every code the brute-force nearest E5M2 value of x * 2^-e; the
+    E4M3 format of the same quantiser equals quant_mxfp8."""
+    x = mx_inputs(24, 256, 30 + rule)
+    q, s = oracle.quant_mx8(x, 1, rule)
+    O = oracle.load()
+    for r in range(x.shape[0]):
+        for b in range(x.shape[1] // 32):
+            blk = x[r, b * 32:(b + 1) * 32]
+            e = O.or_mx8_scale_exp(float(np.abs(blk).max()), rule, 1)
+            assert s[r, b] == e + 127
+            scaled = (blk.astype(np.float64) * 2.0 ** -e).astype(np.float32)
+            np.testing.assert_array_equal(q[r, b * 32:(b + 1) * 32], nearest_codes_e5m2(scaled))
+    q8, s8 = oracle.quant_mx8(x, 0, rule)
+    q0, s0 = oracle.quant_mxfp8(x, rule)
+    np.testing.assert_array_equal(q8, q0)
+    np.testing.assert_array_equal(s8, s0)
+
+
+def test_mx_e5m2_floor_rule_saturates_block_max():
+    x = mx_inputs(16, 256, 7)[4:]
+    q, s = oracle.quant_mx8(x, 1, 0)
+    for r in range(x.shape[0]):
+        for b in range(8):
+            blk = x[r, b * 32:(b + 1) * 32]
+            i = int(np.argmax(np.abs(blk)))
+            assert q[r, b * 32 + i] & 0x7F == 0x7B
