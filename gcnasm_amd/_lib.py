@@ -191,6 +191,7 @@ SIGNATURES = {
     "ga_shuffle_weight_16x16_device": (_i, [_vp, _vp, _i, _i, _vp]),
     "ga_shuffle_scale_device": (_i, [_vp, _vp, _i, _i, _i, _i, _vp]),
     "ga_quant_mxfp8": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
+    "ga_quant_mx8": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "ga_quant_mxfp4": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp]),
     "ga_quant_fp8_1x128": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ga_quant_fp8_128x128": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
@@ -200,6 +201,8 @@ SIGNATURES = {
     "ga_kernel_launch": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _sz, _vp]),
     "ga_kernel_launch_ws_handle": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp, _vp]),
     "ga_kernel_launch_noalloc": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _vp]),
+    "ga_kernel_launch_fmt": (_i, [_i, ctypes.POINTER(F4gemmKargs), _i, _i, _i, _i, _i, _vp, _sz,
+                                  _vp]),
     "ga_mxfp8_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
                            ctypes.POINTER(_i), ctypes.POINTER(LaunchDesc), _vp]),
     "ga_mxfp4_gemm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,

@@ -119,12 +119,21 @@ __device__ __forceinline__ void wait_lgkmcnt0()
 // carry K [64+16g, 64+16g+16). The scale byte (chosen by OPSEL) of the scale
 // VGPR of lane 16*b + r applies to row r, K [32b, 32b+32). Output: lane l
 // holds D[4*(l/16) + j][l%16], j = 0..3.
-template <int OPSEL_A, int OPSEL_B>
+// FMT_A / FMT_B: the operands' f8f6f4 format codes, 0 E4M3 or 1 E5M2 (one
+// byte per element either way, so the lane layout is the same).
+template <int OPSEL_A, int OPSEL_B, int FMT_A = 0, int FMT_B = 0>
 __device__ __forceinline__ v4f mfma_mx16(v8i a, v8i b, v4f c, int sa, int sb)
 {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, OPSEL_A, sa, OPSEL_B,
-                                                            sb);
+    static_assert(FMT_A >= 0 && FMT_A <= 1 && FMT_B >= 0 && FMT_B <= 1, "8-bit formats");
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, OPSEL_A, sa,
+                                                            OPSEL_B, sb);
 }
+
+// A GEMM's operand formats as one template value F = fmt(A) | fmt(B) << 1
+// (0 E4M3, 1 E5M2). The kernels put B on the MFMA's first operand, so its
+// format is the instruction's first code.
+constexpr int fmt_of_a(int F) { return F & 1; }
+constexpr int fmt_of_b(int F) { return (F >> 1) & 1; }
 
 // Same with fp4 (e2m1) operands: lane l = 16*g + r holds row r, K
 // [32g, 32g+32) in its first 16 bytes (two elements per byte, low nibble
@@ -215,6 +224,25 @@ __device__ __forceinline__ uint32_t e4m3_encode4(float a, float b, float c, floa
     return r;
 }
 
+// Four E5M2 (bf8) codes as one dword, same results as the oracle's E5M2
+// encode: the hardware converter on inputs clamped to +-57344 (saturation;
+// the converter alone would round past the maximum to inf), NaN -> 0x7F.
+__device__ __forceinline__ uint32_t e5m2_encode4(float a, float b, float c, float d)
+{
+    const float x[4] = {a, b, c, d};
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        y[j] = __builtin_fminf(__builtin_fmaxf(x[j], -57344.0f), 57344.0f);
+    const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(y[0], y[1], 0, false);
+    uint32_t r = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(y[2], y[3], lo, true);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        if (x[j] != x[j])
+            r = (r & ~(0xFFu << (8 * j))) | (0x7Fu << (8 * j));
+    return r;
+}
+
 // Four e2m1 codes as 16 bits (element j in bits 4j..4j+3), same results as
 // e2m1_encode: the hardware converter (v_cvt_scalef32_pk_fp4_f32, scale 1)
 // on inputs clamped to +-6, NaN inputs replaced by a zero of their sign.
@@ -274,6 +302,12 @@ __device__ __forceinline__ int mx_scale_exp_t(float amax, int rule)
 __device__ __forceinline__ int mx_scale_exp(float amax, int rule)
 {
     return mx_scale_exp_t<0x600000u, 8>(amax, rule);
+}
+
+// E5M2: 57344 = 1.75 * 2^15.
+__device__ __forceinline__ int mx5_scale_exp(float amax, int rule)
+{
+    return mx_scale_exp_t<0x600000u, 15>(amax, rule);
 }
 
 // E2M1: 6 = 1.5 * 2^2.

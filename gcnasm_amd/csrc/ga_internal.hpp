@@ -49,8 +49,8 @@ void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk
 // into registers, K slices summed in the workgroup (no workspace). Results
 // equal the tile kernels' (one fp32 chain of 128-K steps per slice).
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz);
-void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,
-                      hipStream_t stream);
+void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int fmt,
+                      int num_cu, hipStream_t stream);
 // 17-64 rows, each wave over ng (2-8) 16-column groups and one K slice, the
 // slices in separate workgroups (gemm_mx_decode.hip): mx_decode_split_groups
 // gives ng for the shape (0: not this path); with gdz > 1 the slices write
@@ -58,7 +58,13 @@ void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, 
 // split-K reduce, with gdz = 1 the kernel applies the epilogue.
 int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu);
 void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream);
+                            int fmt, float* ws, const ga_splitk_ws_handle* wsh,
+                            hipStream_t stream);
+// fmt (the decode entry points and launch_mx_pp_fmt): MXFP8 operand element
+// formats, fmt(A) | fmt(B) << 1 with 0 E4M3, 1 E5M2; 0 for MXFP4.
+// 256x256 eight-wave kernel with operand formats fmt, grid of its own tiles.
+void launch_mx_pp_fmt(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                      int gdz, bool bps, int fmt, hipStream_t stream);
 
 // Compute units of the current device (queried once per device).
 ga_status device_cu_count(int* num_cu);

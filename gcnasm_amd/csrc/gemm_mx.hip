@@ -920,14 +920,24 @@ namespace ga {
 
 // ga_kernel_launch with the split-K workspace given either as a buffer
 // (workspace, workspace_bytes; NULL: the library-owned one) or as a device
-// slot read by the kernels at entry (wsh; graph-capture safe).
+// slot read by the kernels at entry (wsh; graph-capture safe), and the
+// operand element formats fmt = fmt(A) | fmt(B) << 1 (0 E4M3, 1 E5M2; MXFP8
+// kernels only). With fmt != 0 the rows above the decode path run the
+// 256x256 kernel whatever the entry's tile: every MXFP8 kernel computes the
+// same fp32 chain of 128-K steps per K slice, so the tile is not visible in
+// the output.
 static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
                                void* workspace, size_t workspace_bytes,
-                               const ga_splitk_ws_handle* wsh, void* stream)
+                               const ga_splitk_ws_handle* wsh, void* stream, int fmt = 0)
 {
     if (!args || idx < 0 || idx >= mx_registry_total())
         return fail(GA_ERR_ARG, "kernel_launch: bad kernel index %d", idx);
     const MxKernel& k = *mx_registry_get(idx);
+    if (fmt < 0 || fmt > 3)
+        return fail(GA_ERR_ARG, "kernel_launch: element formats must be 0 (E4M3) or 1 (E5M2)");
+    if (fmt != 0 && k.elem_bits != 8)
+        return fail(GA_ERR_ARG, "kernel_launch: element formats apply to the MXFP8 kernels "
+                                "(kernel %d holds e2m1 operands)", idx);
     const int M = (int)args->M, N = (int)args->N, K = (int)args->K;
     if (M <= 0 || N <= 0 || K <= 0 || !args->ptr_A || !args->ptr_B || !args->ptr_D ||
         !args->ptr_ScaleA || !args->ptr_ScaleB)
@@ -997,7 +1007,7 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
     const int split_groups = decode ? mx_decode_split_groups(*args, gdz, num_cu) : 0;
     if (decode && split_groups == 0) {
         // few rows: stream B, K slices summed inside the kernel (no workspace)
-        launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, num_cu, s);
+        launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, fmt, num_cu, s);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;
     }
@@ -1034,7 +1044,9 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
     }
     if (split_groups > 0)
         launch_mx_decode_split(*args, gdz, split_groups, k.cfg.bpreshuffle != 0, k.elem_bits == 4,
-                               ws, wsh, s);
+                               fmt, ws, wsh, s);
+    else if (fmt != 0)
+        launch_mx_pp_fmt(*args, ws, gdz > 1 ? wsh : nullptr, gdz, k.cfg.bpreshuffle != 0, fmt, s);
     else
         k.launch(*args, ws, gdz > 1 ? wsh : nullptr, gdx, gdy, gdz, s);
     GA_HIP_CHECK(hipGetLastError());
@@ -1079,6 +1091,17 @@ ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int g
     if (gdz > 1 && !ws_handle)
         return fail(GA_ERR_ARG, "kernel_launch_ws_handle: null workspace slot");
     return kernel_launch(idx, args, gdx, gdy, gdz, nullptr, 0, ws_handle, stream);
+}
+
+ga_status ga_kernel_launch_fmt(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
+                               int fmt_a, int fmt_b, void* workspace, size_t workspace_bytes,
+                               void* stream)
+{
+    if (fmt_a < 0 || fmt_a > 1 || fmt_b < 0 || fmt_b > 1)
+        return fail(GA_ERR_ARG, "kernel_launch_fmt: formats must be 0 (E4M3) or 1 (E5M2), got "
+                                "%d, %d", fmt_a, fmt_b);
+    return kernel_launch(idx, args, gdx, gdy, gdz, workspace, workspace_bytes, nullptr, stream,
+                         fmt_a | (fmt_b << 1));
 }
 
 } // extern "C"

@@ -60,7 +60,8 @@ struct DecCfg {
 // Uniform byte offsets as SGPR operands.
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
-template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0>
+// F: the operands' 8-bit element formats (fmt_of_a / fmt_of_b; 0 for MXFP4).
+template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0, int F = 0>
 __global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP, XS>::MAX_WAVES * 64)))
 void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__ ws,
                       const ga_splitk_ws_handle* __restrict__ wsh)
@@ -200,8 +201,8 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                         acc[c][i] = mfma_mx16_fp4<0, 0>(hi16(fb[j][c]), hi16(fa[j][i]), acc[c][i],
                                                         (int)(sb >> 16), (int)(sa >> 16));
                     } else {
-                        acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
-                                                    (int)sa);
+                        acc[c][i] = mfma_mx16<0, 0, fmt_of_b(F), fmt_of_a(F)>(
+                            fb[j][c], fa[j][i], acc[c][i], (int)sb, (int)sa);
                     }
                 }
             }
@@ -235,8 +236,8 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                         acc[c][i] = mfma_mx16_fp4<0, 0>(hi16(fb[j][c]), hi16(fa[j][i]), acc[c][i],
                                                         (int)(sb >> 16), (int)(sa >> 16));
                     } else {
-                        acc[c][i] = mfma_mx16<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
-                                                    (int)sa);
+                        acc[c][i] = mfma_mx16<0, 0, fmt_of_b(F), fmt_of_a(F)>(
+                            fb[j][c], fa[j][i], acc[c][i], (int)sb, (int)sa);
                     }
                 }
                 if (c > 0) {
@@ -372,7 +373,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
 
 // Workgroups: one per CU (more when a CU's share needs over MAX_WAVES
 // waves), each with ceil(share / NG) column tasks x ks slices (ks <= MAX_WAVES).
-template <int TM, int NG, bool BPS, bool FP4, bool DEEP = false>
+template <int TM, int NG, bool BPS, bool FP4, bool DEEP = false, int F = 0>
 void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
@@ -381,8 +382,8 @@ void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t str
     nwg = std::max(nwg, (groups + NG * max_tasks - 1) / (NG * max_tasks));
     const int share = (groups + nwg - 1) / nwg;
     const int tasks = (share + NG - 1) / NG;
-    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP>), dim3(nwg), dim3(64 * tasks * ks), 0,
-                       stream, args, nwg, ks, nullptr, nullptr);
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP, 0, F>), dim3(nwg),
+                       dim3(64 * tasks * ks), 0, stream, args, nwg, ks, nullptr, nullptr);
 }
 
 // Split variant: one wave of NG groups per workgroup per K slice, grid
@@ -397,47 +398,47 @@ constexpr int xs_depth()
     return 1 + 63 / loads > 4 ? 4 : 1 + 63 / loads;
 }
 
-template <int TM, int NG, bool BPS, bool FP4>
+template <int TM, int NG, bool BPS, bool FP4, int F>
 void launch_dec_xs(const ga_f4gemm_kargs& args, int gdz, float* ws, const ga_splitk_ws_handle* wsh,
                    hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
     const int tasks = (groups + NG - 1) / NG;
-    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, false, xs_depth<TM, NG, FP4>()>),
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, false, xs_depth<TM, NG, FP4>(), F>),
                        dim3(tasks, gdz), dim3(64), 0, stream, args, tasks, 1, ws, wsh);
 }
 
-template <int TM, bool BPS, bool FP4>
+template <int TM, bool BPS, bool FP4, int F>
 void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
                       const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
-    if (!BPS) // row-major B: the two extremes only
+    if (!BPS || F != 0) // row-major B, and E5M2 operands: the two extremes only
         ng = ng <= 2 ? 2 : 8;
     switch (ng) {
-    case 2: launch_dec_xs<TM, 2, BPS, FP4>(args, gdz, ws, wsh, stream); break;
-    case 4: launch_dec_xs<TM, 4, BPS, FP4>(args, gdz, ws, wsh, stream); break;
-    case 5: launch_dec_xs<TM, 5, BPS, FP4>(args, gdz, ws, wsh, stream); break;
-    case 6: launch_dec_xs<TM, 6, BPS, FP4>(args, gdz, ws, wsh, stream); break;
-    case 7: launch_dec_xs<TM, 7, BPS, FP4>(args, gdz, ws, wsh, stream); break;
-    default: launch_dec_xs<TM, 8, BPS, FP4>(args, gdz, ws, wsh, stream); break;
+    case 2: launch_dec_xs<TM, 2, BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    case 4: launch_dec_xs<TM, (F ? 8 : 4), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    case 5: launch_dec_xs<TM, (F ? 8 : 5), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    case 6: launch_dec_xs<TM, (F ? 8 : 6), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    case 7: launch_dec_xs<TM, (F ? 8 : 7), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    default: launch_dec_xs<TM, 8, BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
     }
 }
 
-template <bool BPS, bool FP4>
+template <bool BPS, bool FP4, int F>
 void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream_t stream)
 {
     const int tm = ((int)args.M + 15) / 16;
     if (tm == 1)
-        launch_dec<1, 2, BPS, FP4>(args, gdz, num_cu, stream);
+        launch_dec<1, 2, BPS, FP4, false, F>(args, gdz, num_cu, stream);
     else if (tm == 2) {
         // 17-32 rows: six steps in flight for one two-group task per CU and
         // long K, as for 64 rows below
         const int groups = (int)args.N / 16;
         const int steps = (int)args.K / (FP4 ? 256 : 128) / gdz;
         if (gdz <= 4 && steps >= 64 && groups > num_cu && (groups + 1) / 2 <= num_cu)
-            launch_dec<2, 2, BPS, FP4, true>(args, gdz, num_cu, stream);
+            launch_dec<2, 2, BPS, FP4, true, F>(args, gdz, num_cu, stream);
         else
-            launch_dec<2, 2, BPS, FP4>(args, gdz, num_cu, stream);
+            launch_dec<2, 2, BPS, FP4, false, F>(args, gdz, num_cu, stream);
     }
     else {
         // 33-64 rows (measured on MI355X, MXFP8 / MXFP4 at M = 33 and 64):
@@ -449,11 +450,11 @@ void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream
         const int groups = (int)args.N / 16;
         const int steps = (int)args.K / (FP4 ? 256 : 128) / gdz;
         if (groups <= num_cu)
-            launch_dec<4, 1, BPS, FP4>(args, gdz, num_cu, stream);
+            launch_dec<4, 1, BPS, FP4, false, F>(args, gdz, num_cu, stream);
         else if (gdz <= 4 && steps >= 64 && (groups + 1) / 2 <= num_cu)
-            launch_dec<4, 2, BPS, FP4, true>(args, gdz, num_cu, stream);
+            launch_dec<4, 2, BPS, FP4, true, F>(args, gdz, num_cu, stream);
         else
-            launch_dec<4, 2, BPS, FP4>(args, gdz, num_cu, stream);
+            launch_dec<4, 2, BPS, FP4, false, F>(args, gdz, num_cu, stream);
     }
 }
 
@@ -482,41 +483,58 @@ int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
     return ng;
 }
 
-void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream)
+namespace {
+
+template <bool BPS, bool FP4, int F>
+void launch_split_t(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
+                    const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
-    const bool rows64 = args.M > 32;
+    if (args.M > 32)
+        launch_dec_xs_ng<4, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
+    else
+        launch_dec_xs_ng<2, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
+}
+
+template <bool FP4, int F>
+void launch_both(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, float* ws,
+                 const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
+{
+    if (ng > 0)
+        bps ? launch_split_t<true, FP4, F>(args, gdz, ng, ws, wsh, stream)
+            : launch_split_t<false, FP4, F>(args, gdz, ng, ws, wsh, stream);
+    else
+        bps ? launch_dec_rows<true, FP4, F>(args, gdz, num_cu, stream)
+            : launch_dec_rows<false, FP4, F>(args, gdz, num_cu, stream);
+}
+
+// ng > 0: the split variant (ws / wsh), else the in-workgroup kernel.
+void launch_any(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4, int fmt,
+                float* ws, const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
+{
     if (fp4) {
-        if (bps)
-            rows64 ? launch_dec_xs_ng<4, true, true>(args, gdz, ng, ws, wsh, stream)
-                   : launch_dec_xs_ng<2, true, true>(args, gdz, ng, ws, wsh, stream);
-        else
-            rows64 ? launch_dec_xs_ng<4, false, true>(args, gdz, ng, ws, wsh, stream)
-                   : launch_dec_xs_ng<2, false, true>(args, gdz, ng, ws, wsh, stream);
-    } else {
-        if (bps)
-            rows64 ? launch_dec_xs_ng<4, true, false>(args, gdz, ng, ws, wsh, stream)
-                   : launch_dec_xs_ng<2, true, false>(args, gdz, ng, ws, wsh, stream);
-        else
-            rows64 ? launch_dec_xs_ng<4, false, false>(args, gdz, ng, ws, wsh, stream)
-                   : launch_dec_xs_ng<2, false, false>(args, gdz, ng, ws, wsh, stream);
+        launch_both<true, 0>(args, gdz, ng, bps, ws, wsh, num_cu, stream);
+        return;
+    }
+    switch (fmt) {
+    case 1: launch_both<false, 1>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
+    case 2: launch_both<false, 2>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
+    case 3: launch_both<false, 3>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
+    default: launch_both<false, 0>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
     }
 }
 
-void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int num_cu,
-                      hipStream_t stream)
+} // namespace
+
+void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
+                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
-    if (fp4) {
-        if (bps)
-            launch_dec_rows<true, true>(args, gdz, num_cu, stream);
-        else
-            launch_dec_rows<false, true>(args, gdz, num_cu, stream);
-    } else {
-        if (bps)
-            launch_dec_rows<true, false>(args, gdz, num_cu, stream);
-        else
-            launch_dec_rows<false, false>(args, gdz, num_cu, stream);
-    }
+    launch_any(args, gdz, ng, bps, fp4, fmt, ws, wsh, 0, stream);
+}
+
+void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int fmt,
+                      int num_cu, hipStream_t stream)
+{
+    launch_any(args, gdz, 0, bps, fp4, fmt, nullptr, nullptr, num_cu, stream);
 }
 
 } // namespace ga

@@ -192,7 +192,7 @@ struct PpArgs {
 // step reads one whole shuffled scale dword per 32-row block.
 // Two quadrants with shared A fragments: acc0 += A x B0, acc1 += A x B1
 // (16 MFMAs at raised issue priority).
-template <bool FP4>
+template <bool FP4, int F>
 __device__ __forceinline__ void mma_two(v4f (&acc0)[4][2], v4f (&acc1)[4][2], const v8i (&a)[4],
                                         const v8i (&b0)[2], const v8i (&b1)[2],
                                         const uint32_t (&sa)[2], uint32_t sb0, uint32_t sb1)
@@ -209,8 +209,8 @@ __device__ __forceinline__ void mma_two(v4f (&acc0)[4][2], v4f (&acc1)[4][2], co
                     acc[i][t] = mfma_mx16_fp4<2 + (t & 1), 2 + (i & 1)>(
                         hi16(b[t]), hi16(a[i]), acc[i][t], (int)sb, (int)sa[i >> 1]);
                 } else {
-                    acc[i][t] = mfma_mx16<(t & 1), (i & 1)>(b[t], a[i], acc[i][t], (int)sb,
-                                                            (int)sa[i >> 1]);
+                    acc[i][t] = mfma_mx16<(t & 1), (i & 1), fmt_of_b(F), fmt_of_a(F)>(
+                        b[t], a[i], acc[i][t], (int)sb, (int)sa[i >> 1]);
                 }
             });
         });
@@ -232,7 +232,7 @@ __device__ __forceinline__ void part_sync()
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool BPS, bool FP4>
+template <bool BPS, bool FP4, int F>
 __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ ws,
                                         char* smem, int tile_m, int tile_n)
 {
@@ -396,7 +396,7 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
             read_b<0>(rb, P, fb0);
             read_b<1>(rb, P, fb1);
             part_sync<8 + kS>();
-            mma_two<FP4>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
+            mma_two<FP4, F>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
             part_sync<8 + kS>();
             // Y
             issue_a(L, smem, 0, s + 2, wave);
@@ -411,7 +411,7 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
             read_sa<1, FP4>(rb, r0, hb, sa);
             read_a<1>(rb, P, fa);
             part_sync<8 + kS>();
-            mma_two<FP4>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
+            mma_two<FP4, F>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
             part_sync<8 + kS>();
             r0 = r1;
         }
@@ -489,7 +489,8 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
 // pass, so each workgroup stays on the XCD map_tile assigns its tiles to).
 // The epilogue stores of one tile drain while the next tile's first copies
 // are in flight, instead of behind a workgroup exit and a new launch.
-template <bool BPS, bool FP4>
+// F: the operands' 8-bit element formats (fmt_of_a / fmt_of_b; 0 for MXFP4).
+template <bool BPS, bool FP4, int F = 0>
 __global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
 void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws,
                   const ga_splitk_ws_handle* __restrict__ wsh, int tiles_x, int tiles_y)
@@ -519,7 +520,7 @@ void mx_pp_kernel(ga_f4gemm_kargs args, float* __restrict__ ws,
     for (int lin = blockIdx.x; lin < ntiles; lin += gridDim.x) {
         int tile_m, tile_n;
         map_tile_lin(lin, tiles_x, tiles_y, kPpGroupM, tile_m, tile_n);
-        pp_tile<BPS, FP4>(a, ws, smem, tile_m, tile_n);
+        pp_tile<BPS, FP4, F>(a, ws, smem, tile_m, tile_n);
     }
     wait_vmcnt<0>(); // copies of steps past the last slice land before exit
 }
@@ -567,6 +568,34 @@ void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk
 {
     hipLaunchKernelGGL((mx_pp_kernel<false, true>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
                        0, stream, args, ws, wsh, gdx, gdy);
+}
+
+namespace {
+
+template <bool BPS, int F>
+void launch_pp_f(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh, int gdz,
+                 hipStream_t stream)
+{
+    const int gdx = ((int)args.N + 255) / 256, gdy = ((int)args.M + 255) / 256;
+    hipLaunchKernelGGL((mx_pp_kernel<BPS, false, F>), dim3(pp_grid(gdx * gdy), 1, gdz), dim3(kNT),
+                       0, stream, args, ws, wsh, gdx, gdy);
+}
+
+} // namespace
+
+void launch_mx_pp_fmt(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                      int gdz, bool bps, int fmt, hipStream_t stream)
+{
+    switch (fmt) {
+    case 1: bps ? launch_pp_f<true, 1>(args, ws, wsh, gdz, stream)
+                : launch_pp_f<false, 1>(args, ws, wsh, gdz, stream); break;
+    case 2: bps ? launch_pp_f<true, 2>(args, ws, wsh, gdz, stream)
+                : launch_pp_f<false, 2>(args, ws, wsh, gdz, stream); break;
+    case 3: bps ? launch_pp_f<true, 3>(args, ws, wsh, gdz, stream)
+                : launch_pp_f<false, 3>(args, ws, wsh, gdz, stream); break;
+    default: bps ? launch_pp_f<true, 0>(args, ws, wsh, gdz, stream)
+                 : launch_pp_f<false, 0>(args, ws, wsh, gdz, stream); break;
+    }
 }
 
 } // namespace ga

@@ -100,7 +100,8 @@ __device__ __forceinline__ uint32_t group_max_dpp(uint32_t a)
 // A 1x32 block is LPB = 32/EPL lanes of EPL elements (16-byte loads where the
 // layout allows); each lane handles U blocks, BPP = 256/LPB blocks apart, so U
 // independent loads are in flight per lane before the first reduction.
-template <int IN, int EPL, bool FP4, int U>
+// E5: E5M2 elements instead of E4M3 (FP4 false).
+template <int IN, int EPL, bool FP4, int U, bool E5 = false>
 __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ x, int rows,
                                                        int K, int ld_x, uint8_t* __restrict__ q,
                                                        int ld_q, uint8_t* __restrict__ s,
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ 
         const float amax = __uint_as_float(group_max_dpp<LPB>(amax_n<EPL>(v[u])));
         if (!ok[u])
             continue;
-        const int e = FP4 ? mx4_scale_exp(amax, rule) : mx_scale_exp(amax, rule);
+        const int e = FP4 ? mx4_scale_exp(amax, rule)
+                          : (E5 ? mx5_scale_exp(amax, rule) : mx_scale_exp(amax, rule));
         uint8_t* qrow = q + (size_t)rr[u] * ld_q;
         if constexpr (FP4) {
             float t[EPL];
@@ -146,13 +148,16 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ 
 #pragma unroll
             for (int j = 0; j < EPL; j++)
                 t[j] = ldexpf(v[u][j], -e);
+            auto enc4 = [](float p, float q_, float r, float w) {
+                return E5 ? e5m2_encode4(p, q_, r, w) : e4m3_encode4(p, q_, r, w);
+            };
             if constexpr (EPL == 8) {
                 uint2 w;
-                w.x = e4m3_encode4(t[0], t[1], t[2], t[3]);
-                w.y = e4m3_encode4(t[4], t[5], t[6], t[7]);
+                w.x = enc4(t[0], t[1], t[2], t[3]);
+                w.y = enc4(t[4], t[5], t[6], t[7]);
                 *(uint2*)(qrow + bb[u] * 32 + sub * 8) = w;
             } else {
-                *(uint32_t*)(qrow + bb[u] * 32 + sub * 4) = e4m3_encode4(t[0], t[1], t[2], t[3]);
+                *(uint32_t*)(qrow + bb[u] * 32 + sub * 4) = enc4(t[0], t[1], t[2], t[3]);
             }
         }
         if (sub == 0)
@@ -414,7 +419,7 @@ static bool bf16_wide(int in_dtype, const void* x, int ld_x, const void* q, int 
            ld_q % store_align == 0 && ((uintptr_t)q % store_align) == 0;
 }
 
-template <bool FP4>
+template <bool FP4, bool E5 = false>
 static void launch_quant_mx(int in_dtype, bool wide, long long blocks, hipStream_t st,
                             const void* x, int rows, int K, int ld_x, uint8_t* q, int ld_q,
                             uint8_t* s, int ld_s, int rule)
@@ -422,14 +427,14 @@ static void launch_quant_mx(int in_dtype, bool wide, long long blocks, hipStream
     const int epl = in_dtype == GA_IN_F32 ? 4 : (wide ? 8 : 4);
     const unsigned grid = grid1d(blocks, (256 / (32 / epl)) * kQU);
     if (in_dtype == GA_IN_F32)
-        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_F32, 4, FP4, kQU>), dim3(grid), dim3(256), 0, st,
-                           x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_F32, 4, FP4, kQU, E5>), dim3(grid), dim3(256), 0,
+                           st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
     else if (wide)
-        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 8, FP4, kQU>), dim3(grid), dim3(256), 0,
-                           st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 8, FP4, kQU, E5>), dim3(grid), dim3(256),
+                           0, st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
     else
-        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 4, FP4, kQU>), dim3(grid), dim3(256), 0,
-                           st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 4, FP4, kQU, E5>), dim3(grid), dim3(256),
+                           0, st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
 }
 
 static ga_status check_in(int in_dtype)
@@ -441,22 +446,32 @@ static ga_status check_in(int in_dtype)
 
 extern "C" {
 
-ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x, void* q,
-                         int ld_q, void* scales, int ld_s, int scale_rule, void* stream)
+ga_status ga_quant_mx8(const void* x, int in_dtype, int rows, int K, int ld_x, void* q, int ld_q,
+                       void* scales, int ld_s, int scale_rule, int fmt, void* stream)
 {
     if (check_in(in_dtype) != GA_OK)
         return GA_ERR_ARG;
     if (!x || !q || !scales || rows <= 0 || K <= 0 || ld_x < K || ld_q < K || ld_s < K / 32 ||
-        scale_rule < 0 || scale_rule > 2)
-        return fail(GA_ERR_ARG, "quant_mxfp8: bad argument");
+        scale_rule < 0 || scale_rule > 2 || fmt < 0 || fmt > 1)
+        return fail(GA_ERR_ARG, "quant_mx8: bad argument (fmt 0 E4M3 or 1 E5M2)");
     if (K % 32 || ld_x % 4 || ld_q % 4)
-        return fail(GA_ERR_SHAPE, "quant_mxfp8: K %% 32, ld_x %% 4 and ld_q %% 4 must be 0");
+        return fail(GA_ERR_SHAPE, "quant_mx8: K %% 32, ld_x %% 4 and ld_q %% 4 must be 0");
     long long blocks = (long long)rows * (K / 32);
-    launch_quant_mx<false>(in_dtype, bf16_wide(in_dtype, x, ld_x, q, ld_q, 8), blocks,
-                           (hipStream_t)stream, x, rows, K, ld_x, (uint8_t*)q, ld_q,
-                           (uint8_t*)scales, ld_s, scale_rule);
+    const bool wide = bf16_wide(in_dtype, x, ld_x, q, ld_q, 8);
+    if (fmt == 1)
+        launch_quant_mx<false, true>(in_dtype, wide, blocks, (hipStream_t)stream, x, rows, K,
+                                     ld_x, (uint8_t*)q, ld_q, (uint8_t*)scales, ld_s, scale_rule);
+    else
+        launch_quant_mx<false>(in_dtype, wide, blocks, (hipStream_t)stream, x, rows, K, ld_x,
+                               (uint8_t*)q, ld_q, (uint8_t*)scales, ld_s, scale_rule);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
+}
+
+ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x, void* q,
+                         int ld_q, void* scales, int ld_s, int scale_rule, void* stream)
+{
+    return ga_quant_mx8(x, in_dtype, rows, K, ld_x, q, ld_q, scales, ld_s, scale_rule, 0, stream);
 }
 
 ga_status ga_quant_mxfp4(const void* x, int in_dtype, int rows, int K, int ld_x, void* q,

@@ -231,11 +231,26 @@ class Kernel:
         d = ld.to_c()
         return lib().ga_kernel_workspace_bytes(self.idx, ctypes.byref(d), M, N)
 
-    def launch(self, args, gdx, gdy, gdz, stream=None, workspace=None, ws_handle=None):
+    def launch(self, args, gdx, gdy, gdz, stream=None, workspace=None, ws_handle=None,
+               fmt_a=0, fmt_b=0):
         """Kernel::launch. The split-K workspace is `workspace` (a tensor; None:
         the library's own), or with `ws_handle` (a flatmm_splitk.WorkspaceHandle
         or a device slot address) found through that slot when the kernels run
-        (ga_kernel_launch_ws_handle: safe to capture into a HIP graph)."""
+        (ga_kernel_launch_ws_handle: safe to capture into a HIP graph).
+        fmt_a / fmt_b: the MXFP8 operands' element formats, 0 E4M3 (default)
+        or 1 E5M2 (ga_kernel_launch_fmt; with a workspace buffer or the
+        library's)."""
+        if fmt_a or fmt_b:
+            if ws_handle is not None:
+                raise ValueError("element formats take a workspace buffer, not a slot")
+            ws_ptr, ws_bytes = None, 0
+            if workspace is not None:
+                ws_ptr = _ptr(workspace)
+                ws_bytes = workspace.numel() * workspace.element_size()
+            check(lib().ga_kernel_launch_fmt(self.idx, ctypes.byref(args), gdx, gdy, gdz,
+                                             int(fmt_a), int(fmt_b), ws_ptr, ws_bytes,
+                                             _stream_handle(stream)))
+            return
         if ws_handle is not None:
             addr = getattr(ws_handle, "address", ws_handle)
             check(lib().ga_kernel_launch_ws_handle(self.idx, ctypes.byref(args), gdx, gdy, gdz,

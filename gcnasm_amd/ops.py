@@ -39,6 +39,18 @@ def quant_mxfp8(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
     return q, s
 
 
+def quant_mx8(x, fmt, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
+    """x [rows, K] -> (q uint8 [rows, K] codes of format fmt: 0 E4M3, 1 E5M2;
+    scales uint8 [rows, K/32] E8M0, unshuffled); rule numbers as for MXFP8
+    with the format's maximum (448 or 57344)."""
+    rows, K = _rows(x)
+    q = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+    check(lib().ga_quant_mx8(x.data_ptr(), _in_dtype(x), rows, K, x.stride(0), q.data_ptr(), K,
+                             s.data_ptr(), K // 32, scale_rule, int(fmt), _stream_handle(stream)))
+    return q, s
+
+
 def quant_mxfp4(x, scale_rule=_lib.GA_MX_SCALE_FLOOR_448, stream=None):
     """x [rows, K] -> (q uint8 [rows, K/2] packed e2m1, low nibble = even element;
     scales uint8 [rows, K/32] E8M0, unshuffled). Rule numbers as for MXFP8 with

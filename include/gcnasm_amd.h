@@ -281,6 +281,13 @@ ga_status ga_shuffle_scale_device(const void* src, void* dst, int rows, int cols
 ga_status ga_quant_mxfp8(const void* x, int in_dtype, int rows, int K, int ld_x,
                          void* q, int ld_q, void* scales, int ld_s, int scale_rule,
                          void* stream);
+/* ga_quant_mxfp8 with the element format: fmt 0 = E4M3 (ga_quant_mxfp8), 1 =
+ * E5M2 (bf8, for ga_kernel_launch_fmt): round to nearest even, saturate to
+ * +-57344, NaN -> 0x7F, scale rules with the E5M2 maximum 57344 = 1.75 * 2^15
+ * in place of 448 (rule 2: floor(log2(amax)) - 15). No counterpart in the
+ * reference (its quantisers produce E4M3 or e2m1). */
+ga_status ga_quant_mx8(const void* x, int in_dtype, int rows, int K, int ld_x, void* q,
+                       int ld_q, void* scales, int ld_s, int scale_rule, int fmt, void* stream);
 /* MXFP4 quantiser: x [rows, K] -> q [rows, K/2] bytes of OCP e2m1 codes
  * (element 2i in the low nibble of byte i, asm_f4gemm/README.md:99; round to
  * nearest even, saturate to +-6, NaN -> signed zero; row stride ld_q bytes)
@@ -339,7 +346,8 @@ ga_status ga_kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, int gd
  * buffer. The slot must hold gdz * M * N floats (ga_kernel_workspace_bytes):
  * for a slot made by ga_ws_handle_create this is checked on the host
  * (GA_ERR_WORKSPACE) outside capture; a shorter slot met by the kernels makes
- * them write nothing. gdz == 1 (and the M <= 64 paths) use no workspace. */
+ * them write nothing. gdz == 1 uses no workspace, nor does a split at 1-16
+ * rows (the decode kernel sums its K slices in the workgroup). */
 ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
                                      int gdz, const ga_splitk_ws_handle* ws_handle,
                                      void* stream);
@@ -356,6 +364,23 @@ ga_status ga_kernel_launch_ws_handle(int idx, const ga_f4gemm_kargs* args, int g
  * threads) race: serialise them. Otherwise as ga_kernel_launch. */
 ga_status ga_kernel_launch_noalloc(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy,
                                    int gdz, void* stream);
+
+/* ga_kernel_launch with the 8-bit element format of each MXFP8 operand:
+ * fmt_a (A) and fmt_b (B) are f8f6f4 format codes, 0 = E4M3 (fp8, what
+ * ga_kernel_launch takes) or 1 = E5M2 (bf8), in any pairing; the E8M0 1x32
+ * scales, layouts, preshuffle and split-K are those of ga_kernel_launch (an
+ * E5M2 element is one byte too). Replaces the format-code arguments of the
+ * reference's scaled-MFMA dispatch (wmma_opus_rdna4/opus/opus.hpp:1785-1786,
+ * fmt_a / fmt_b of mfma_scale_f32_16x16x128_f8f6f4) at the GEMM level; the
+ * reference's asm_f4gemm kernels have fixed formats. idx must be an MXFP8
+ * registry entry (GA_ERR_ARG for MXFP4 kernels and other codes). Rows above
+ * the decode path (M > 64) run the 256x256 eight-wave kernel whichever tile
+ * idx names (the grid arguments are checked against idx as usual); every
+ * MXFP8 kernel computes the same fp32 chain per K slice, so the output does
+ * not depend on the tile. fmt_a = fmt_b = 0 is ga_kernel_launch. */
+ga_status ga_kernel_launch_fmt(int idx, const ga_f4gemm_kargs* args, int gdx, int gdy, int gdz,
+                               int fmt_a, int fmt_b, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* One-call MXFP8 GEMM: select_kernel + make_launch + fill_args + launch.
  * log2_k_split as in ga_select_kernel. Writes the chosen kernel index and

@@ -157,3 +157,23 @@ def test_flatmm_splitk_validation_without_gpu():
     assert l.ga_ws_handle_query(0x1234, None, None) == _lib.GA_ERR_ARG
     assert l.ga_ws_handle_destroy(0x1234) == _lib.GA_ERR_ARG
     assert l.ga_ws_handle_create(None) == _lib.GA_ERR_ARG
+
+
+def test_element_formats_are_validated_without_gpu():
+    """ga_kernel_launch_fmt: format codes other than 0 (E4M3) / 1 (E5M2), and
+    any E5M2 request on an MXFP4 kernel, are GA_ERR_ARG before a device call;
+    a valid request still meets the usual argument checks (bad grid)."""
+    l = _lib.lib()
+    args = _lib.F4gemmKargs()
+    l.ga_fill_args(ctypes.byref(args), 8, None, 8, 8, 8, 8, 64, 64, 256, 64, 8, 8, 1.0, 0.0, 0)
+    for fa, fb in ((2, 0), (0, 2), (-1, 0), (4, 4)):
+        assert l.ga_kernel_launch_fmt(0, ctypes.byref(args), 1, 1, 1, fa, fb, None, 0, None) == \
+            _lib.GA_ERR_ARG
+        assert b"E5M2" in l.ga_last_error()
+    idx = ctypes.c_int()
+    assert l.ga_kernel_find(b"ga_mxfp4_bf16_BpreShuffle_256x256", ctypes.byref(idx)) == 0
+    assert l.ga_kernel_launch_fmt(idx.value, ctypes.byref(args), 1, 1, 1, 1, 0, None, 0,
+                                  None) == _lib.GA_ERR_ARG
+    assert b"e2m1" in l.ga_last_error()
+    assert l.ga_kernel_launch_fmt(0, ctypes.byref(args), 99, 1, 1, 1, 1, None, 0, None) == \
+        _lib.GA_ERR_ARG

@@ -159,3 +159,62 @@ def test_prepare_matches_host_path(dev):
     np.testing.assert_array_equal(b.scales.cpu().numpy(),
                                   oracle.shuffle_scale(s, N, K // 32, sh.scale_b_rows(),
                                                        sh.scale_cols()))
+
+
+@pytest.mark.parametrize("rule", [0, 1, 2])
+@pytest.mark.parametrize("in_bf16", [False, True])
+def test_quant_mx8_e5m2(dev, rule, in_bf16):
+    """MX 1x32 with E5M2 elements (ga_quant_mx8 fmt 1) byte for byte against
+    the oracle, codes and scales, fp32 and bf16 inputs, a partial 16-byte tail
+    of rows; fmt 0 equals the E4M3 quantiser."""
+    rows, K = 77, 1056
+    x = oracle.gen_mx_input(rows, K, 55 + rule, 1.0, 6)
+    x[0, :32] = 0.0
+    x[1, 5] = np.nan
+    x[2, :32] = 57344.0
+    if in_bf16:
+        xb = oracle.to_bf16_bits(x)
+        t = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+        x = oracle.bf16_bits_to_f32(xb)
+    else:
+        t = torch.from_numpy(x).to(dev)
+    q, s = ops.quant_mx8(t, 1, rule)
+    q8, s8 = ops.quant_mx8(t, 0, rule)
+    q0, s0 = ops.quant_mxfp8(t, rule)
+    torch.cuda.synchronize()
+    qo, so = oracle.quant_mx8(x, 1, rule)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(q8.cpu().numpy(), q0.cpu().numpy())
+    np.testing.assert_array_equal(s8.cpu().numpy(), s0.cpu().numpy())
+
+
+def test_e5m2_encoder_every_bf16_value(dev):
+    """Every bf16 bit pattern of magnitude <= 57344 (and every NaN) through the
+    device E5M2 encoder at scale 1: each 32-block holds 57344 first, so the
+    floor rule gives exponent 0, then 31 of the test values."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = oracle.bf16_bits_to_f32(bits)
+    keep = np.isnan(vals) | (np.abs(vals) <= 57344.0)
+    v = vals[keep]
+    per = 31
+    nblk = (len(v) + per - 1) // per
+    pad = np.zeros(nblk * per, np.float32)
+    pad[:len(v)] = v
+    blocks = np.concatenate([np.full((nblk, 1), 57344.0, np.float32), pad.reshape(nblk, per)],
+                            axis=1)
+    rows = (nblk + 31) // 32
+    x = np.zeros((rows * 32, 32), np.float32)
+    x[:nblk] = blocks
+    x = x.reshape(rows, 32 * 32)
+    xb = oracle.to_bf16_bits(x)
+    assert np.array_equal(oracle.bf16_bits_to_f32(xb)[np.isfinite(x)], x[np.isfinite(x)])
+    t = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    q, s = ops.quant_mx8(t, 1, 0)
+    torch.cuda.synchronize()
+    xf = oracle.bf16_bits_to_f32(xb)
+    sc = s.cpu().numpy()[:, :]
+    assert np.all(sc.reshape(-1)[:nblk] == 127)
+    np.testing.assert_array_equal(q.cpu().numpy(), oracle.quant_mx8(xf, 1, 0)[0])
+    np.testing.assert_array_equal(q.cpu().numpy().reshape(-1, 32)[:nblk, 1:].reshape(-1)[:len(v)],
+                                  oracle.e5m2_encode(v))
