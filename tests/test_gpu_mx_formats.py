@@ -153,3 +153,20 @@ def test_default_formats_equal_plain_launch(dev):
         outs.append(D[:M].view(torch.int16).cpu().numpy().view(np.uint16))
     np.testing.assert_array_equal(outs[1], outs[0])
     check(outs[1], qa, sa, qb, sb, 0, 0, l2, "formats 0x0 via ga_kernel_launch_fmt")
+
+
+@pytest.mark.parametrize("l2", [0, 1])
+def test_every_tile_writes_the_same_bits(dev, l2):
+    """Above the decode path every MXFP8 kernel (all tiles, preshuffled and
+    row-major B) chains the same 128-K MFMA steps per K slice from zero, so
+    the bf16 output is bit-identical whichever entry runs; this is what lets
+    ga_kernel_launch_fmt run the 256x256 kernel for any index. Checked over
+    the whole manifest (split entries at l2 = 1), and against the oracle."""
+    M, N, K = 300, 784, 1536
+    qa, sa, qb, sb = operands(M, N, K, 0, 0, seed=31 + l2)
+    cfgs = [c for c in f4gemm.manifest() if l2 == 0 or c.splitK]
+    outs = [run_fmt(dev, qa, sa, qb, sb, c, l2, 0, 0)[0] for c in cfgs]
+    for c, got in zip(cfgs[1:], outs[1:]):
+        np.testing.assert_array_equal(got, outs[0], err_msg="%s vs %s" % (c.knl_name,
+                                                                         cfgs[0].knl_name))
+    check(outs[0], qa, sa, qb, sb, 0, 0, l2, "every tile l2=%d" % l2)
