@@ -38,6 +38,9 @@ constexpr int kSBase = kOperandBytes;
 constexpr int kLdsBs = kSBase + kSRing * kSSlot;
 static_assert(kLdsBs <= 160 * 1024, "LDS budget");
 constexpr int kBsGroupM = 4;
+// fp32 epilogue staging: 128 rows of 1024 + 16 bytes (the 16 rows of one
+// ds_write_b128 quarter-wave start 4 banks apart).
+constexpr int kStagePitchF32 = 1040;
 
 struct BsLoad {
     __amdgpu_buffer_rsrc_t ra, rb, rs; // rs: SFA (waves 0-3) or SFB (waves 4-7)
@@ -363,6 +366,61 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
     if constexpr (MODE == PS_TENSOR)
         tscale = ((const float*)ka.ptr_sfa)[0] * ((const float*)ka.ptr_sfb)[0];
     char* pc = (char*)ka.ptr_c + (size_t)b * ka.stride_c_batch * (OUT == GA_DTYPE_F32 ? 4 : 2);
+    // Whole interior tiles go through LDS so that the global stores write
+    // whole rows (1 KB fp32 or 512 B bf16 per instruction instead of 16 rows
+    // x 64 or 32 B): bf16 in one pass, fp32 in two passes of 128 rows.
+    const int ldc = ka.stride_c;
+    const bool staged = m0 + 256 <= M && n0 + 256 <= N && ((uintptr_t)pc & 15) == 0 &&
+                        (ldc & (OUT == GA_DTYPE_F32 ? 3 : 7)) == 0;
+    if (staged) {
+        barrier_lds(); // every wave's operand and scale reads are done
+        if constexpr (OUT == GA_DTYPE_F32) {
+            static_assert(128 * kStagePitchF32 <= kLdsBs, "fp32 staging fits in LDS");
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                if (h)
+                    barrier_lds(); // rows of pass 0 read before pass 1 overwrites them
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int t = 0; t < 2; t++) {
+                            const v4f v = acc[2 * h + qq][i][t] * tscale;
+                            const int row = grp * 64 + i * 16 + (lane & 15);
+                            const int col = qq * 128 + simd * 32 + t * 16 + (lane >> 4) * 4;
+                            *(v4f*)(smem + row * kStagePitchF32 + col * 4) = v;
+                        }
+                barrier_lds();
+                float* dst = (float*)pc + (size_t)(m0 + h * 128) * ldc + n0;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = wave * 16 + r;
+                    const v4i d = *(const v4i*)(smem + row * kStagePitchF32 + lane * 16);
+                    *(v4i*)(dst + (size_t)row * ldc + lane * 4) = d;
+                }
+            }
+        } else {
+            static_assert(kStageBytes <= kLdsBs, "bf16 staging fits in LDS");
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const v4f v = acc[q][i][t] * tscale;
+                        const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) |
+                                            ((uint32_t)f32_to_bf16(v[1]) << 16);
+                        const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) |
+                                            ((uint32_t)f32_to_bf16(v[3]) << 16);
+                        stage_put(smem, (q >> 1) * 128 + grp * 64 + i * 16 + (lane & 15),
+                                  (q & 1) * 128 + simd * 32 + t * 16 + (lane >> 4) * 4, lo, hi);
+                    }
+            barrier_lds();
+            stage_store(smem, (uint16_t*)pc + (size_t)m0 * ldc + n0, ldc, wave, lane);
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
 #pragma unroll

@@ -119,6 +119,95 @@ def test_blockscale_deepseek_configs(dev, shape):
     assert_parity(st, "bs bf16 %s" % (shape,))
 
 
+def _rows_checked(M):
+    return np.unique(np.concatenate([np.arange(4), np.arange(M - 4, M), tile_rows(M)]))
+
+
+@pytest.mark.parametrize("group_n", [128, 1])
+@pytest.mark.parametrize("shape,ldc_pad", [((4100, 4100, 256), 0), ((4100, 4100, 384), 12),
+                                           ((2304, 7680, 512), 0), ((2304, 7680, 128), 0),
+                                           ((4100, 4098, 256), 2)])
+def test_blockscale_more_tiles_than_cus(dev, group_n, shape, ldc_pad):
+    """More 256x256 tiles than CUs (more than one round of workgroups), K of
+    one to four 128-K groups, ragged last tiles in M and N, a row stride above
+    N whose padding must stay untouched and no write past row M, fp32 and bf16
+    C, N % 4 != 0 included. Checked on the first and last rows and one row of
+    every 256-row tile, against the oracle."""
+    M, N, K = shape
+    ldc = N + ldc_pad
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + N + K, group_n=group_n)
+    rows = _rows_checked(M)
+    qa_r = np.ascontiguousarray(qa[0][rows])
+    sfa_r = np.ascontiguousarray(sfa[0][:, rows])
+    want = expect_bs(qa_r, qb[0], sfa_r, sfb[0], group_n, M_full=M)
+    absdot = oracle.blockscale_absdot(qa_r, qb[0], sfa_r, sfb[0], group_n)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    A, B, SA, SB = t(qa), t(qb), t(sfa), t(sfb)
+    for dt in (torch.float32, torch.bfloat16):
+        # one spare row past M: nothing may be written there either
+        Cbuf = torch.full((M + 1, ldc), float("nan"), dtype=dt, device=dev)
+        ka = opus_gemm.make_kargs(A, B, Cbuf, SA, SB, M, N, K, 1, group_n)
+        ka.stride_c = ldc
+        ka.stride_c_batch = M * ldc
+        print("bs %s ldc=%d group_n=%d %s" % (shape, ldc, group_n, dt), flush=True)
+        opus_gemm.gemm_a8w8_blockscale(ka, opus_gemm._out_dtype(Cbuf), group_n)
+        torch.cuda.synchronize()
+        if dt == torch.float32:
+            full = Cbuf.cpu().numpy()
+            ok, st = f32_compare(full[:M, :N][rows], want, absdot=absdot)
+            pad = full[:, N:]
+            tail = full[M]
+        else:
+            full = Cbuf.view(torch.int16).cpu().numpy().view(np.uint16)
+            ok, st = bf16_compare(full[:M, :N][rows], oracle.to_bf16_bits(want), absdot)
+            pad = oracle.bf16_bits_to_f32(full[:, N:])
+            tail = oracle.bf16_bits_to_f32(full[M])
+        assert_parity(st, "bs %s ldc=%d g%d %s" % (shape, ldc, group_n, dt))
+        assert np.all(np.isnan(pad)), "row padding written"
+        assert np.all(np.isnan(tail)), "row past M written"
+
+
+def test_blockscale_batched_more_tiles_than_cus(dev):
+    """Batched launch with more tiles per batch entry than CUs (2 x 289
+    tiles)."""
+    M, N, K, batch = 4100, 4100, 256, 2
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=41, batch=batch)
+    C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
+    rows = _rows_checked(M)
+    for b in range(batch):
+        qa_r = np.ascontiguousarray(qa[b][rows])
+        sfa_r = np.ascontiguousarray(sfa[b][:, rows])
+        want = expect_bs(qa_r, qb[b], sfa_r, sfb[b], 128, M_full=M, batch=batch)
+        absdot = oracle.blockscale_absdot(qa_r, qb[b], sfa_r, sfb[b], 128)
+        ok, st = f32_compare(C[b].cpu().numpy()[rows], want, absdot=absdot)
+        assert_parity(st, "batched, more tiles than CUs %d" % b)
+
+
+@pytest.mark.parametrize("shape", [(4100, 4100, 512), (2304, 7680, 256)])
+def test_per_tensor_more_tiles_than_cus(dev, shape):
+    """Per-tensor with more tiles than CUs (one fp32 chain, scale in the
+    epilogue), ragged tiles, fp32 and bf16 C, rows checked as above."""
+    M, N, K = shape
+    xa = oracle.randn(M * K, 31).reshape(M, K)
+    xb = oracle.randn(N * K, 32).reshape(N, K)
+    qa, sa = oracle.quant_fp8_per_tensor(xa)
+    qb, sb = oracle.quant_fp8_per_tensor(xb)
+    rows = _rows_checked(M)
+    want = expect_pt(np.ascontiguousarray(qa[rows]), qb, sa[0], sb[0], M_full=M)
+    absdot = oracle.fp8_absdot(np.ascontiguousarray(qa[rows]), qb) * float(sa[0]) * float(sb[0])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    for dt in (torch.float32, torch.bfloat16):
+        C = torch.full((M, N), float("nan"), dtype=dt, device=dev)
+        opus_gemm.per_tensor_gemm(t(qa), t(qb), t(sa), t(sb), C)
+        torch.cuda.synchronize()
+        if dt == torch.float32:
+            ok, st = f32_compare(C.cpu().numpy()[rows], want, absdot=absdot)
+        else:
+            ok, st = bf16_compare(C.view(torch.int16).cpu().numpy().view(np.uint16)[rows],
+                                  oracle.to_bf16_bits(want), absdot)
+        assert_parity(st, "per-tensor, more tiles than CUs %s %s" % (shape, dt))
+
+
 def test_blockscale_batched(dev):
     M, N, K, batch = 128, 384, 512, 3
     qa, qb, sfa, sfb = ds_operands(M, N, K, seed=5, batch=batch)
