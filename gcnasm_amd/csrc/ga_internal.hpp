@@ -71,6 +71,15 @@ ga_status device_cu_count(int* num_cu);
 // 256x256 eight-wave fp32-scaled FP8 GEMM (gemm_bs_pp.hip); mode 0 = block
 // scale GROUP_N 128, 1 = GROUP_N 1, 2 = per-tensor.
 void launch_bs_pp(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, hipStream_t stream);
+// The same kernel's stream-K form (batch 1): workgroups it would use on
+// num_cu CUs (0: the whole-tile form is the better one), its workspace
+// (per-tile counters, zero between calls, then 2 * nwg fp32 partial tiles),
+// the counters' share of it, and the launch.
+int bs_sk_workgroups(const ga_opus_gemm_kargs& ka, int num_cu);
+size_t bs_sk_counter_bytes(const ga_opus_gemm_kargs& ka);
+size_t bs_sk_workspace_bytes(const ga_opus_gemm_kargs& ka, int nwg);
+void launch_bs_pp_sk(const ga_opus_gemm_kargs& ka, int mode, int out_dtype, int nwg, void* ws,
+                     hipStream_t stream);
 // The same GEMMs for up to 64 rows, streaming B (gemm_bs_decode.hip); same
 // mode numbering.
 ga_status launch_bs_decode(const ga_opus_gemm_kargs& ka, int mode, int out_dtype,

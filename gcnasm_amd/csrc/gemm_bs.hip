@@ -360,14 +360,7 @@ static ga_status check_scales(const ga_opus_gemm_kargs* ka, int group_n)
     return GA_OK;
 }
 
-} // namespace ga
-
-using namespace ga;
-
-extern "C" {
-
-ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype,
-                                  void* stream)
+static ga_status check_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype)
 {
     ga_status st = check_kargs(kargs);
     if (st != GA_OK)
@@ -382,7 +375,31 @@ ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, 
         return fail(GA_ERR_SHAPE, "stride_sfb must be >= N for GROUP_N 1");
     if (kargs->stride_sfa < kargs->m)
         return fail(GA_ERR_SHAPE, "stride_sfa must be >= M (SFA is [K/128, M])");
-    st = check_scales(kargs, group_n);
+    return check_scales(kargs, group_n);
+}
+
+// Workgroups of the stream-K form for these kargs on this device (0: the
+// call runs whole tiles).
+static ga_status bs_stream_k_plan(const ga_opus_gemm_kargs& ka, int* nwg)
+{
+    int num_cu = 0;
+    ga_status st = device_cu_count(&num_cu);
+    if (st != GA_OK)
+        return st;
+    *nwg = bs_path(ka, num_cu) == BS_PATH_PP ? bs_sk_workgroups(ka, num_cu) : 0;
+    return GA_OK;
+}
+
+} // namespace ga
+
+using namespace ga;
+
+extern "C" {
+
+ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype,
+                                  void* stream)
+{
+    ga_status st = check_blockscale(kargs, group_n, out_dtype);
     if (st != GA_OK)
         return st;
     hipStream_t s = (hipStream_t)stream;
@@ -391,6 +408,51 @@ ga_status ga_gemm_a8w8_blockscale(const ga_opus_gemm_kargs* kargs, int group_n, 
                                          : dispatch_bs<BS_GROUP128, GA_DTYPE_BF16>(*kargs, s);
     return out_dtype == GA_DTYPE_F32 ? dispatch_bs<BS_GROUP1, GA_DTYPE_F32>(*kargs, s)
                                      : dispatch_bs<BS_GROUP1, GA_DTYPE_BF16>(*kargs, s);
+}
+
+ga_status ga_blockscale_stream_k(const ga_opus_gemm_kargs* kargs, int* workgroups)
+{
+    if (!kargs || !workgroups)
+        return fail(GA_ERR_ARG, "ga_blockscale_stream_k: null argument");
+    if (kargs->m <= 0 || kargs->n <= 0 || kargs->k <= 0 || kargs->batch <= 0 ||
+        kargs->k % 128 != 0)
+        return fail(GA_ERR_SHAPE, "ga_blockscale_stream_k: M, N, K, batch > 0, K %% 128 == 0");
+    return bs_stream_k_plan(*kargs, workgroups);
+}
+
+ga_status ga_blockscale_workspace_bytes(const ga_opus_gemm_kargs* kargs, size_t* bytes)
+{
+    if (!bytes)
+        return fail(GA_ERR_ARG, "ga_blockscale_workspace_bytes: null argument");
+    int nwg = 0;
+    ga_status st = ga_blockscale_stream_k(kargs, &nwg);
+    if (st != GA_OK)
+        return st;
+    *bytes = bs_sk_workspace_bytes(*kargs, nwg);
+    return GA_OK;
+}
+
+ga_status ga_gemm_a8w8_blockscale_ws(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream)
+{
+    ga_status st = check_blockscale(kargs, group_n, out_dtype);
+    if (st != GA_OK)
+        return st;
+    int nwg = 0;
+    st = bs_stream_k_plan(*kargs, &nwg);
+    if (st != GA_OK)
+        return st;
+    if (nwg > 0 && workspace) {
+        const size_t need = bs_sk_workspace_bytes(*kargs, nwg);
+        if (workspace_bytes < need)
+            return fail(GA_ERR_WORKSPACE, "blockscale workspace holds %zu bytes, need %zu",
+                        workspace_bytes, need);
+        launch_bs_pp_sk(*kargs, group_n == 128 ? BS_GROUP128 : BS_GROUP1, out_dtype, nwg,
+                        workspace, (hipStream_t)stream);
+        GA_HIP_CHECK(hipGetLastError());
+        return GA_OK;
+    }
+    return ga_gemm_a8w8_blockscale(kargs, group_n, out_dtype, stream);
 }
 
 ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_per_slice)

@@ -53,9 +53,53 @@ def _out_dtype(c):
     raise TypeError("C must be float32 or bfloat16")
 
 
-def gemm_a8w8_blockscale(kargs, out_dtype, group_n=128, stream=None):
-    check(lib().ga_gemm_a8w8_blockscale(ctypes.byref(kargs), group_n, out_dtype,
-                                        _stream_handle(stream)))
+def gemm_a8w8_blockscale(kargs, out_dtype, group_n=128, stream=None, workspace=None):
+    """gemm_a8w8_blockscale_kernel; with `workspace` (a zero-filled device
+    tensor of workspace_bytes(kargs) bytes, kept zero-filled by the calls)
+    ga_gemm_a8w8_blockscale_ws, which may run the stream-K form."""
+    if workspace is None:
+        check(lib().ga_gemm_a8w8_blockscale(ctypes.byref(kargs), group_n, out_dtype,
+                                            _stream_handle(stream)))
+        return
+    check(lib().ga_gemm_a8w8_blockscale_ws(ctypes.byref(kargs), group_n, out_dtype,
+                                           ctypes.c_void_p(workspace.data_ptr()),
+                                           workspace.numel() * workspace.element_size(),
+                                           _stream_handle(stream)))
+
+
+def workspace_bytes(kargs):
+    """Bytes ga_gemm_a8w8_blockscale_ws can use for these kargs (0: none)."""
+    n = ctypes.c_size_t(0)
+    check(lib().ga_blockscale_workspace_bytes(ctypes.byref(kargs), ctypes.byref(n)))
+    return n.value
+
+
+def stream_k_workgroups(m, n, k, batch=1):
+    """Workgroups of the stream-K form ga_gemm_a8w8_blockscale_ws runs for
+    these sizes on the current device (0: whole tiles)."""
+    ka = opus_gemm_kargs()
+    ka.m, ka.n, ka.k, ka.batch = m, n, k, batch
+    w = ctypes.c_int(0)
+    check(lib().ga_blockscale_stream_k(ctypes.byref(ka), ctypes.byref(w)))
+    return w.value
+
+
+def stream_k_cuts(m, n, k, workgroups):
+    """{(tile_m, tile_n): [first 128-K group of each K piece]} of the stream-K
+    plan (ga_blockscale_stream_k's documented order) with `workgroups`
+    workgroups: a tile's K pieces are summed in this order."""
+    tn, tm, G = (n + 255) // 256, (m + 255) // 256, k // 128
+    T = tn * tm * G
+    begins = [v * T // workgroups for v in range(workgroups)]
+    cuts = {}
+    for t in range(tn * tm):
+        band = 4 * tn
+        first_m = 4 * (t // band)
+        h = min(tm - first_m, 4)
+        r = t % band
+        key = (first_m + r % h, r // h)
+        cuts[key] = [0] + sorted(b - t * G for b in begins if t * G < b < (t + 1) * G)
+    return cuts
 
 
 def gemm_a8w8_1x128x1_blockscale(kargs, out_dtype, stream=None):
@@ -66,13 +110,14 @@ def fp8_gemm(kargs, out_dtype, stream=None):
     check(lib().ga_fp8_gemm_per_tensor(ctypes.byref(kargs), out_dtype, _stream_handle(stream)))
 
 
-def blockscale_gemm(a, b, sfa, sfb, c, group_n=128, stream=None):
-    """Tensor-level wrapper: a [B,M,K] or [M,K] uint8 E4M3, c fp32/bf16."""
+def blockscale_gemm(a, b, sfa, sfb, c, group_n=128, stream=None, workspace=None):
+    """Tensor-level wrapper: a [B,M,K] or [M,K] uint8 E4M3, c fp32/bf16;
+    `workspace` as for gemm_a8w8_blockscale."""
     batch = a.shape[0] if a.dim() == 3 else 1
     m, k = a.shape[-2], a.shape[-1]
     n = b.shape[-2]
     ka = make_kargs(a, b, c, sfa, sfb, m, n, k, batch, group_n)
-    gemm_a8w8_blockscale(ka, _out_dtype(c), group_n, stream)
+    gemm_a8w8_blockscale(ka, _out_dtype(c), group_n, stream, workspace)
     return c
 
 

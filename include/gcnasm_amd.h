@@ -423,6 +423,40 @@ ga_status ga_fp8_gemm_per_tensor(const ga_opus_gemm_kargs* kargs, int out_dtype,
  * chain. Lets a caller (or a test) reproduce the rounding exactly. */
 ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_per_slice);
 
+/* ga_gemm_a8w8_blockscale with a caller workspace, which lets long-K
+ * problems whose 256x256 tiles would keep few CUs busy (batch 1, more than
+ * 64 rows, tiles for at most 40 % of the CUs, at least 16 128-K groups per
+ * CU; e.g. 2048x2560x8192: 80 tiles on 256 CUs, 103 -> 84 us on MI355X)
+ * run in stream-K form: every CU takes an equal share of the tiles' 128-K
+ * groups, and a tile cut between CUs is summed from fp32 partials in K
+ * order by the last CU to finish it (the DeepSeek configuration shapes are
+ * not among them: their partial traffic costs as much as the balance
+ * gains). The reference's kernel has no split, and its cross-workgroup
+ * counter (wmma_opus_rdna4/opus/opus.hpp:1296-1304) spins, where here nobody
+ * waits. workspace: ga_blockscale_workspace_bytes bytes (up to about 128
+ * MiB), zero-filled before its first use (hipMemset) and left zero-filled by
+ * every call; calls that overlap in time must not share it. workspace NULL,
+ * or a shape the whole-tile kernel suits, runs exactly
+ * ga_gemm_a8w8_blockscale; a workspace that is too small is
+ * GA_ERR_WORKSPACE. Summation order: ga_blockscale_stream_k. */
+ga_status ga_gemm_a8w8_blockscale_ws(const ga_opus_gemm_kargs* kargs, int group_n, int out_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace ga_gemm_a8w8_blockscale_ws can use for these kargs on the
+ * current device (0: it runs the whole-tile kernel). */
+ga_status ga_blockscale_workspace_bytes(const ga_opus_gemm_kargs* kargs, size_t* bytes);
+
+/* Stream-K plan of ga_gemm_a8w8_blockscale_ws (given a workspace) on the
+ * current device: *workgroups = P, or 0 when that call runs whole tiles.
+ * With G = K/128 and T = tiles * G, iteration t*G + g is 128-K group g of
+ * tile t, and workgroup v computes iterations [floor(v*T/P),
+ * floor((v+1)*T/P)). Tiles are numbered in bands of four tile rows, column
+ * by column within a band: with r = t % (4*tiles_n) and h the band's height
+ * (4, or fewer in the last band), tile_m = 4*(t / (4*tiles_n)) + r % h and
+ * tile_n = r / h. A tile's K is cut where its iterations change workgroup;
+ * each piece is one fp32 chain and the pieces are added in K order. */
+ga_status ga_blockscale_stream_k(const ga_opus_gemm_kargs* kargs, int* workgroups);
+
 /* splitk_reduce_kernel: C[b, m, n] = sum_s ws[s, b, m, n] (+ bias[n]) in fp32,
  * cast to out_dtype. ws is [split_k, batch, padded_M, padded_N] fp32. bias
  * may be NULL; bias_dtype is GA_DTYPE_BF16/F32; bias_stride_batch 0 means

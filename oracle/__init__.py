@@ -69,6 +69,8 @@ _SIGS = {
     "or_gemm_mx8_mfma": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp, _i, _i]),
     "or_gemm_blockscale_mfma": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
                                        _i, _i, _i]),
+    "or_gemm_blockscale_mfma_cuts": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
+                                            _i, _i, _vp, _i]),
     "or_gemm_per_tensor_mfma": (None, [_vp, _vp, _f, _f, _vp, _i, _i, _i, _i]),
     "or_splitk_reduce": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _i]),
     "or_a16w16_slices": (None, [_i, _i, _vp, _vp]),
@@ -451,9 +453,10 @@ def gemm_mx_mfma(qa, sa, qb, sb, log2_k_split=0, alpha=1.0):
     return D
 
 
-def gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n=128, gps=0):
+def gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n=128, gps=0, cuts=None):
     """Block-scale GEMM (fp32) with the MFMA's step sum; K slices of gps
-    128-K groups summed in order (0: one slice)."""
+    128-K groups summed in order (0: one slice), or K cut before the 128-K
+    groups listed in `cuts` (first 0)."""
     qa = np.ascontiguousarray(qa)
     qb = np.ascontiguousarray(qb)
     sfa = np.ascontiguousarray(sfa, dtype=np.float32)
@@ -461,9 +464,15 @@ def gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n=128, gps=0):
     M, K = qa.shape
     N = qb.shape[0]
     C = np.empty((M, N), dtype=np.float32)
+    ssfb = _sfb_stride(N, K, group_n) if group_n == 128 else sfb.shape[1]
+    if cuts is not None:
+        c = np.ascontiguousarray(cuts, dtype=np.int32)
+        assert c[0] == 0 and np.all(np.diff(c) > 0) and c[-1] < K // 128, cuts
+        load().or_gemm_blockscale_mfma_cuts(p(qa), p(qb), p(sfa), p(sfb), p(C), M, N, K, K, K, N,
+                                            sfa.shape[1], ssfb, group_n, p(c), len(c))
+        return C
     load().or_gemm_blockscale_mfma(p(qa), p(qb), p(sfa), p(sfb), p(C), M, N, K, K, K, N,
-                                   sfa.shape[1], _sfb_stride(N, K, group_n) if group_n == 128
-                                   else sfb.shape[1], group_n, gps)
+                                   sfa.shape[1], ssfb, group_n, gps)
     return C
 
 

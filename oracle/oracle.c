@@ -1080,6 +1080,37 @@ void or_gemm_blockscale_mfma(const uint8_t* A, const uint8_t* B, const float* sf
         }
 }
 
+/* or_gemm_blockscale_mfma with K cut at explicit 128-K group indices: piece c
+ * covers groups [cuts[c], cuts[c+1]) (the last one up to K/128), cuts[0] = 0
+ * and increasing; each piece is one fp32 chain and the pieces are added in
+ * order. The K pieces of the library's stream-K form (one list per tile). */
+void or_gemm_blockscale_mfma_cuts(const uint8_t* A, const uint8_t* B, const float* sfa,
+                                  const float* sfb, float* C, int M, int N, int K, int lda,
+                                  int ldb, int ldc, int stride_sfa, int stride_sfb, int group_n,
+                                  const int* cuts, int ncuts)
+{
+    f8_tab_init();
+    int G = K / 128;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            const uint8_t* a = A + (size_t)i * lda;
+            const uint8_t* b = B + (size_t)j * ldb;
+            float total = 0.0f;
+            for (int c = 0; c < ncuts; c++) {
+                const int g1 = c + 1 < ncuts ? cuts[c + 1] : G;
+                float acc = 0.0f;
+                for (int g = cuts[c]; g < g1; g++) {
+                    float p = mfma_fp8_step(a, b, g * 128, g * 128 + 128, NULL, NULL, 0.0f);
+                    float s = sfa[(size_t)g * stride_sfa + i] * sfb_at(sfb, g, j, stride_sfb, group_n);
+                    acc = fmaf(p, s, acc);
+                }
+                total = c == 0 ? acc : total + acc;
+            }
+            C[(size_t)i * ldc + j] = total;
+        }
+}
+
 /* Per-tensor: the MFMA chain over 128-K steps (slices of gps steps summed in
  * slice order), out = fp32(acc * fp32(sa*sb)). */
 void or_gemm_per_tensor_mfma(const uint8_t* A, const uint8_t* B, float sa, float sb, float* C,

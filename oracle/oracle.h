@@ -136,6 +136,10 @@ void or_gemm_mx_mfma(const uint8_t* A, const uint8_t* B, const uint8_t* sA, cons
 void or_gemm_blockscale_mfma(const uint8_t* A, const uint8_t* B, const float* sfa,
                              const float* sfb, float* C, int M, int N, int K, int lda, int ldb,
                              int ldc, int stride_sfa, int stride_sfb, int group_n, int gps);
+void or_gemm_blockscale_mfma_cuts(const uint8_t* A, const uint8_t* B, const float* sfa,
+                                  const float* sfb, float* C, int M, int N, int K, int lda,
+                                  int ldb, int ldc, int stride_sfa, int stride_sfb, int group_n,
+                                  const int* cuts, int ncuts);
 void or_gemm_per_tensor_mfma(const uint8_t* A, const uint8_t* B, float sa, float sb, float* C,
                              int M, int N, int K, int gps);
 

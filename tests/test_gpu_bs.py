@@ -9,6 +9,8 @@ against the reference's own gemm_ref semantics
 (per-product fp32 sum, opus_gemm/block_scale_gemm/..._host.cc:66-90) with the
 reference's absolute tolerance scaled to the output magnitude.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -206,6 +208,114 @@ def test_per_tensor_more_tiles_than_cus(dev, shape):
             ok, st = bf16_compare(C.view(torch.int16).cpu().numpy().view(np.uint16)[rows],
                                   oracle.to_bf16_bits(want), absdot)
         assert_parity(st, "per-tensor, more tiles than CUs %s %s" % (shape, dt))
+
+
+def expect_bs_stream_k(qa, qb, sfa, sfb, group_n, rows, M):
+    """Oracle for ga_gemm_a8w8_blockscale_ws on rows `rows` of [M, N, K]:
+    each 256x256 tile with its own stream-K K pieces (opus_gemm.stream_k_cuts
+    of the library's plan), or the whole-tile kernel's slices without one."""
+    N, K = qb.shape
+    P = opus_gemm.stream_k_workgroups(M, N, K)
+    if P == 0:
+        return expect_bs(qa[rows], qb, sfa[:, rows], sfb, group_n, M_full=M), 0
+    cuts = opus_gemm.stream_k_cuts(M, N, K, P)
+    out = np.empty((len(rows), N), np.float32)
+    for tn in range((N + 255) // 256):
+        cols = slice(256 * tn, min(N, 256 * tn + 256))
+        qb_t = np.ascontiguousarray(qb[cols])
+        sfb_t = np.ascontiguousarray(sfb[2 * tn:2 * tn + 2] if group_n == 128 else sfb[:, cols])
+        for tm in sorted(set(int(r) // 256 for r in rows)):
+            sel = np.nonzero(np.asarray(rows) // 256 == tm)[0]
+            r = np.asarray(rows)[sel]
+            out[sel, cols] = oracle.gemm_blockscale_mfma(
+                np.ascontiguousarray(qa[r]), qb_t, np.ascontiguousarray(sfa[:, r]), sfb_t,
+                group_n, cuts=cuts[(tm, tn)])
+    return out, P
+
+
+def run_bs_ws(dev, qa, qb, sfa, sfb, out_dtype, group_n, ws):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    M, K = qa.shape
+    N = qb.shape[0]
+    C = torch.full((M, N), float("nan"), dtype=out_dtype, device=dev)
+    opus_gemm.blockscale_gemm(t(qa), t(qb), t(sfa), t(sfb), C, group_n, workspace=ws)
+    torch.cuda.synchronize()
+    return C
+
+
+@pytest.mark.parametrize("group_n", [128, 1])
+@pytest.mark.parametrize("shape", [(2048, 2560, 8192), (2100, 2600, 6144), (2304, 2304, 6656),
+                                   (1536, 4096, 8192)])
+def test_blockscale_stream_k(dev, group_n, shape):
+    """ga_gemm_a8w8_blockscale_ws: tile counts that fit the CUs badly run in
+    stream-K form (every CU an equal share of the tiles' 128-K groups; a tile
+    cut between CUs summed from fp32 partials in K order by the last one):
+    long-K shapes whose tiles keep at most 40 % of the CUs busy, with three
+    to five K pieces per tile, ragged edges, at least 16 K groups per CU, fp32 and bf16 C, each tile
+    against the oracle with its own cuts; a second call gives the same bits
+    (the tile counters were left at zero)."""
+    M, N, K = shape
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=M + 3 * N + K, group_n=group_n)
+    qa, qb, sfa, sfb = qa[0], qb[0], sfa[0], sfb[0]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    C0 = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ka = opus_gemm.make_kargs(t(qa[None]), t(qb[None]), C0, t(sfa[None]), t(sfb[None]),
+                              M, N, K, 1, group_n)
+    nbytes = opus_gemm.workspace_bytes(ka)
+    ws = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=dev)
+    rows = _rows_checked(M)
+    want, P = expect_bs_stream_k(qa, qb, sfa, sfb, group_n, rows, M)
+    assert P > 0 and nbytes > 0, "shape %s does not take the stream-K form" % (shape,)
+    absdot = oracle.blockscale_absdot(np.ascontiguousarray(qa[rows]), qb,
+                                      np.ascontiguousarray(sfa[:, rows]), sfb, group_n)
+    for dt in (torch.float32, torch.bfloat16):
+        print("stream-K %s group_n=%d %s P=%d" % (shape, group_n, dt, P), flush=True)
+        C = run_bs_ws(dev, qa, qb, sfa, sfb, dt, group_n, ws)
+        C2 = run_bs_ws(dev, qa, qb, sfa, sfb, dt, group_n, ws)
+        if dt == torch.float32:
+            got = C.cpu().numpy()
+            ok, st = f32_compare(got[rows], want, absdot=absdot)
+            np.testing.assert_array_equal(C2.cpu().numpy().view(np.uint32), got.view(np.uint32))
+        else:
+            got = C.view(torch.int16).cpu().numpy().view(np.uint16)
+            ok, st = bf16_compare(got[rows], oracle.to_bf16_bits(want), absdot)
+            np.testing.assert_array_equal(C2.view(torch.int16).cpu().numpy(), got.view(np.int16))
+        assert_parity(st, "stream-K %s g%d %s" % (shape, group_n, dt))
+    assert int(ws[:((M + 255) // 256) * ((N + 255) // 256) * 4].sum()) == 0, "counters not reset"
+
+
+def test_blockscale_ws_whole_tiles_where_they_fit():
+    """Tile counts that keep over 40 % of the CUs busy (the three DeepSeek
+    configuration shapes: 144, 448 and 1536 tiles) keep the whole-tile
+    kernel with or without a workspace: no stream-K plan, no workspace asked
+    for."""
+    for M, N, K in ((4096, 2112, 7168), (4096, 7168, 2048), (4096, 24576, 1536),
+                    (8192, 8192, 8192), (4096, 1792, 6144)):
+        assert opus_gemm.stream_k_workgroups(M, N, K) == 0, (M, N, K)
+
+
+def test_blockscale_ws_without_workspace_and_short_workspace(dev):
+    """ga_gemm_a8w8_blockscale_ws with no workspace is the plain call, bit for
+    bit; a workspace short of ga_blockscale_workspace_bytes is an error."""
+    M, N, K = 2048, 2560, 8192
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=77)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    A, B, SA, SB = t(qa), t(qb), t(sfa), t(sfb)
+    C1 = torch.full((1, M, N), float("nan"), device=dev)
+    C2 = torch.full((1, M, N), float("nan"), device=dev)
+    opus_gemm.blockscale_gemm(A, B, SA, SB, C1, 128)
+    ka = opus_gemm.make_kargs(A, B, C2, SA, SB, M, N, K, 1, 128)
+    from gcnasm_amd import _lib
+    _lib.check(_lib.lib().ga_gemm_a8w8_blockscale_ws(ctypes.byref(ka), 128, _lib.GA_DTYPE_F32,
+                                                     None, 0, None))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(C2.cpu().numpy().view(np.uint32),
+                                  C1.cpu().numpy().view(np.uint32))
+    need = opus_gemm.workspace_bytes(ka)
+    assert need > 0
+    short = torch.zeros(need - 256, dtype=torch.uint8, device=dev)
+    with pytest.raises(RuntimeError, match="workspace"):
+        opus_gemm.gemm_a8w8_blockscale(ka, _lib.GA_DTYPE_F32, 128, workspace=short)
 
 
 def test_blockscale_batched(dev):

@@ -151,6 +151,45 @@ def test_blockscale_and_per_tensor_slices():
         np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("group_n", [128, 1])
+def test_blockscale_explicit_cuts(group_n):
+    """K cut before explicit 128-K groups (the stream-K pieces of one tile):
+    [0] is the single chain and multiples of gps are the gps slices, bit for
+    bit; uneven cuts equal one call per piece added in fp32 in piece order."""
+    rng = np.random.default_rng(12)
+    M, N, K = 8, 40, 896
+    G = K // 128
+    qa, _ = _mx_data(M, K, rng, False)
+    qb, _ = _mx_data(N, K, rng, False)
+    sfa = rng.uniform(0.5, 2, (G, M)).astype(np.float32)
+    sfb = (rng.uniform(0.5, 2, ((N + 127) // 128, G)) if group_n == 128 else
+           rng.uniform(0.5, 2, (G, N))).astype(np.float32)
+
+    def bits(x):
+        return x.view(np.uint32)
+    one = oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n)
+    np.testing.assert_array_equal(
+        bits(oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n, cuts=[0])), bits(one))
+    for gps in (2, 3):
+        np.testing.assert_array_equal(
+            bits(oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n,
+                                             cuts=list(range(0, G, gps)))),
+            bits(oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n, gps)))
+    cuts = [0, 1, 5]
+    bounds = cuts + [G]
+    want = None
+    for g0, g1 in zip(bounds[:-1], bounds[1:]):
+        ks = slice(128 * g0, 128 * g1)
+        sb = sfb[:, g0:g1] if group_n == 128 else sfb[g0:g1]
+        part = oracle.gemm_blockscale_mfma(
+            np.ascontiguousarray(qa[:, ks]), np.ascontiguousarray(qb[:, ks]),
+            np.ascontiguousarray(sfa[g0:g1]), np.ascontiguousarray(sb), group_n)
+        want = part if want is None else (want + part).astype(np.float32)
+    got = oracle.gemm_blockscale_mfma(qa, qb, sfa, sfb, group_n, cuts=cuts)
+    np.testing.assert_array_equal(bits(got), bits(want))
+    assert not np.array_equal(bits(got), bits(one))  # the cuts change the rounding
+
+
 def test_blockscale_no_truncation_equals_kernel_order_oracle():
     rng = np.random.default_rng(4)
     M, N, K = 16, 200, 512
