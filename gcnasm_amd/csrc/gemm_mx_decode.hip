@@ -72,6 +72,17 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
     constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
     static_assert(kLoadsPerStep * (D - 1) < 64, "vmcnt range");
+    // MXFP8 in-workgroup: a scale dword covers 256 K = two steps, so only the
+    // even ring slots (the even steps: D is even) load scales and the odd
+    // step reuses its even neighbour's, kept from that step's MFMAs. The
+    // wait before slot J's MFMAs counts the D - 1 other slots' loads, issued
+    // after slot J's: D/2 - 1 slots of J's parity and D/2 of the other.
+    constexpr bool kPairScales = !FP4 && XS == 0 && D % 2 == 0;
+    constexpr int kLoadsOdd = kPairScales ? 2 * NG + 2 * TM : kLoadsPerStep;
+    constexpr int kWaitEven =
+        kPairScales ? (D / 2 - 1) * kLoadsPerStep + (D / 2) * kLoadsOdd : (D - 1) * kLoadsPerStep;
+    constexpr int kWaitOdd =
+        kPairScales ? (D / 2) * kLoadsPerStep + (D / 2 - 1) * kLoadsOdd : (D - 1) * kLoadsPerStep;
     // in-workgroup K slices are summed through LDS (<= 8 waves)
     __shared__ __attribute__((aligned(16))) float red[XS > 0 ? 4 : 8 * NG * TM * 256];
     if constexpr (XS > 0) {
@@ -178,23 +189,51 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                 v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
                 fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
             }
-            const uint32_t q = (uint32_t)(FP4 ? s : (s >> 1)) * 256;
+            if constexpr (!kPairScales || j % 2 == 0) {
+                const uint32_t q = (uint32_t)(FP4 ? s : (s >> 1)) * 256;
 #pragma unroll
-            for (int h = 0; h < SA; h++)
-                fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
+                for (int h = 0; h < SA; h++)
+                    fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
 #pragma unroll
-            for (int c = 0; c < NB; c++)
-                fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+                for (int c = 0; c < NB; c++)
+                    fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+            }
         };
+        // The odd step's scale operands, shifted out of the even slot's
+        // registers during the even step: load() refills those registers right
+        // after it, so the odd step cannot read them. The empty asm keeps the
+        // shifted values from being recomputed (which would keep the even
+        // slot's old registers live across the refill).
+        uint32_t osa[TM], osb[NG];
         auto mma = [&](int s, auto J) {
             constexpr int j = decltype(J)::value;
+            constexpr bool odd = kPairScales && j % 2 == 1;
             const uint32_t sh = FP4 ? 0u : (uint32_t)(s & 1) * 16;
+            uint32_t sbv[NG], sav[TM];
 #pragma unroll
-            for (int c = 0; c < NG; c++) {
-                const uint32_t sb = fsb[j][NB == NG ? c : c / 2] >> (sh + 8 * ((cg0 + c) & 1));
+            for (int c = 0; c < NG; c++)
+                sbv[c] = odd ? osb[c] : fsb[j][NB == NG ? c : c / 2] >> (sh + 8 * ((cg0 + c) & 1));
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                sav[i] = odd ? osa[i] : fsa[j][i >> 1] >> (sh + 8 * (i & 1));
+            if constexpr (kPairScales && j % 2 == 0) {
+#pragma unroll
+                for (int c = 0; c < NG; c++) {
+                    osb[c] = fsb[j][NB == NG ? c : c / 2] >> (16 + 8 * ((cg0 + c) & 1));
+                    asm volatile("" : "+v"(osb[c]));
+                }
 #pragma unroll
                 for (int i = 0; i < TM; i++) {
-                    const uint32_t sa = fsa[j][i >> 1] >> (sh + 8 * (i & 1));
+                    osa[i] = fsa[j][i >> 1] >> (16 + 8 * (i & 1));
+                    asm volatile("" : "+v"(osa[i]));
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                const uint32_t sb = sbv[c];
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    const uint32_t sa = sav[i];
                     if constexpr (FP4) {
                         acc[c][i] = mfma_mx16_fp4<0, 0>(fb[j][c], fa[j][i], acc[c][i], (int)sb,
                                                         (int)sa);
@@ -277,7 +316,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         int s = 0;
         for (; s + D <= nsteps; s += D) {
             static_for<D>([&](auto J) {
-                wait_vmcnt<kLoadsPerStep * (D - 1)>();
+                wait_vmcnt<(decltype(J)::value % 2 == 0) ? kWaitEven : kWaitOdd>();
                 if constexpr (XS > 0) {
                     mma_load(s + J, min(s + D + (int)J, nsteps - 1), J);
                 } else {
