@@ -55,10 +55,12 @@ void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, 
 // slices in separate workgroups (gemm_mx_decode.hip): mx_decode_split_groups
 // gives ng for the shape (0: not this path); with gdz > 1 the slices write
 // fp32 partials to the split-K workspace (ws, or the slot wsh) for the
-// split-K reduce, with gdz = 1 the kernel applies the epilogue.
+// split-K reduce, with gdz = 1 the kernel applies the epilogue (33-64 rows:
+// in the shared-A variant, four waves per workgroup sharing A through LDS,
+// sized from num_cu).
 int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu);
 void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            int fmt, float* ws, const ga_splitk_ws_handle* wsh,
+                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, int num_cu,
                             hipStream_t stream);
 // fmt (the decode entry points and launch_mx_pp_fmt): MXFP8 operand element
 // formats, fmt(A) | fmt(B) << 1 with 0 E4M3, 1 E5M2; 0 for MXFP4.

@@ -1044,7 +1044,7 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
     }
     if (split_groups > 0)
         launch_mx_decode_split(*args, gdz, split_groups, k.cfg.bpreshuffle != 0, k.elem_bits == 4,
-                               fmt, ws, wsh, s);
+                               fmt, ws, wsh, num_cu, s);
     else if (fmt != 0)
         launch_mx_pp_fmt(*args, ws, gdz > 1 ? wsh : nullptr, gdz, k.cfg.bpreshuffle != 0, fmt, s);
     else

@@ -60,6 +60,65 @@ struct DecCfg {
 // Uniform byte offsets as SGPR operands.
 __device__ __forceinline__ uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// A K slice's fp32 partials to the split-K workspace, [slice][M][N] (lane
+// holds C[m][n .. n+3], m = 16i + lane%16, n = 16cg + 4(lane/16)), for the
+// groups [cg0, cg0 + ng_here) and the rows below M.
+template <int NG, int TM>
+__device__ __forceinline__ void dec_store_partials(float* ws, const v4f (&acc)[NG][TM], int slice,
+                                                   int cg0, int ng_here, int M, int N, int lane)
+{
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+        if (c >= ng_here)
+            continue;
+        const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = i * 16 + (lane & 15);
+            if (m < M)
+                *(v4f*)(ws + ((size_t)slice * M + m) * N + n) = acc[c][i];
+        }
+    }
+}
+
+// D = alpha * acc (+ beta * C) as bf16, same lane layout and bounds.
+template <int NG, int TM>
+__device__ __forceinline__ void dec_epilogue(const ga_f4gemm_kargs& args, const v4f (&acc)[NG][TM],
+                                             int cg0, int ng_here, int lane)
+{
+    const int M = (int)args.M;
+    const int ldd = (int)args.stride_C0;
+    const float alpha = args.alpha, beta = args.beta;
+    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+        if (c >= ng_here)
+            continue;
+        const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = i * 16 + (lane & 15);
+            if (m >= M)
+                continue;
+            const v4f v = acc[c][i];
+            uint16_t o[4];
+            const uint16_t* cin =
+                use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n : nullptr;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float x = alpha * v[j];
+                if (use_c)
+                    x = x + beta * bf16_to_f32(cin[j]);
+                o[j] = f32_to_bf16(x);
+            }
+            uint2 pk;
+            pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+            pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+            *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+        }
+    }
+}
+
 // F: the operands' 8-bit element formats (fmt_of_a / fmt_of_b; 0 for MXFP4).
 template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0, int F = 0>
 __global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP, XS>::MAX_WAVES * 64)))
@@ -332,24 +391,11 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         });
     }
 
-    // Split variant: this slice's fp32 partials to the workspace, [slice][M][N]
-    // (lane holds C[m][n .. n+3], m = 16i + lane%16, n = 16cg + 4(lane/16));
-    // one slice: the epilogue below.
+    // Split variant: this slice's fp32 partials to the workspace; one slice:
+    // the epilogue below.
     if (XS > 0 && gridDim.y > 1) {
-        if (!live)
-            return;
-#pragma unroll
-        for (int c = 0; c < NG; c++) {
-            if (c >= ng_here)
-                continue;
-            const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
-#pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int m = i * 16 + (lane & 15);
-                if (m < M)
-                    *(v4f*)(ws + ((size_t)slice * M + m) * N + n) = acc[c][i];
-            }
-        }
+        if (live)
+            dec_store_partials<NG, TM>(ws, acc, slice, cg0, ng_here, M, N, lane);
         return;
     }
     // Sum the K slices of each column group in slice order, then the epilogue.
@@ -376,38 +422,262 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                 acc[c][i] = t;
             }
     }
-    if (!live)
-        return;
-    const int ldd = (int)args.stride_C0;
-    const float alpha = args.alpha, beta = args.beta;
-    const bool use_c = beta != 0.0f && args.ptr_C != nullptr;
-#pragma unroll
-    for (int c = 0; c < NG; c++) {
-        if (c >= ng_here)
-            continue;
-        const int n = (cg0 + c) * 16 + (lane >> 4) * 4;
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int m = i * 16 + (lane & 15);
-            if (m >= M)
-                continue;
-            const v4f v = acc[c][i];
-            uint16_t o[4];
-            const uint16_t* cin =
-                use_c ? (const uint16_t*)args.ptr_C + (size_t)m * ldd + n : nullptr;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float x = alpha * v[j];
-                if (use_c)
-                    x = x + beta * bf16_to_f32(cin[j]);
-                o[j] = f32_to_bf16(x);
-            }
-            uint2 pk;
-            pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
-            pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-            *(uint2*)((uint16_t*)args.ptr_D + (size_t)m * ldd + n) = pk;
+    if (live)
+        dec_epilogue<NG, TM>(args, acc, cg0, ng_here, lane);
+}
+
+// Shared-A split variant (33-64 rows). A workgroup of four waves, one per
+// SIMD, takes K slice blockIdx.y of a contiguous range of column groups
+// (nwg equal shares), each wave up to NG of them. Each step's A rows
+// (TM x 16 rows x 128 bytes) go into an LDS ring of D steps with direct-to-LDS
+// loads, 2 * TM / 4 one-KB copies per wave, and every wave reads the whole
+// step from there: a CU reads A once per step for all its columns, and the
+// MFMAs of the 64 rows spread over the four SIMDs. B and the scales stream
+// into registers as in the other variants (ring of D steps per wave).
+// Step u: wait for the wave's loads of step u, barrier (every wave's copies
+// of step u landed, every wave's LDS reads of step u - 1 done), read step u's
+// A, copy step u + D - 1's A into the slot step u - 1 used, MFMAs, then step
+// u + D's B and scales into the registers step u used. MXFP8 scales as in
+// the in-workgroup variant: one dword per pair of steps, loaded on the even
+// step, the odd step's operands shifted out during the even step.
+// One slice applies the epilogue; more write fp32 partials for the split-K
+// reduce (ws, or the slot wsh), as the split variant does.
+template <int TM, int NG, bool BPS, bool FP4, int F>
+struct LaCfg {
+    static constexpr int W = 4;                       // waves per workgroup
+    static constexpr int SA = (TM + 1) / 2;           // A scale dwords per step
+    static constexpr int BPW = 2 * TM / W;            // A copies per wave per step
+    static constexpr int LB = 2 * NG;                 // B loads per step
+    static constexpr int SS = SA + NG;                // scale loads per (even) step
+    // deepest ring whose waits stay within the 63 loads vmcnt counts, at most 8
+    static constexpr int depth()
+    {
+        int d = 2;
+        for (int t = 3; t <= 8; t++) {
+            const bool pair = !FP4 && t % 2 == 0;
+            const int w = LB + (t - 2) * (BPW + LB) + (pair ? SS * t / 2 : SS * (t - 1));
+            if (w < 64)
+                d = t;
         }
+        return d;
     }
+    static constexpr int D = depth();
+    static constexpr bool kPair = !FP4 && D % 2 == 0;
+    // loads issued after the last one step u needs: step u + 1's B and
+    // scales, then D - 2 steps of (A copies, B, scales); the scale loads of
+    // steps u + 1 .. u + D - 1 (the even ones only with pairs)
+    static constexpr int kBase = LB + (D - 2) * (BPW + LB);
+    static constexpr int kWaitEven = kBase + (kPair ? SS * (D - 2) / 2 : SS * (D - 1));
+    static constexpr int kWaitOdd = kBase + (kPair ? SS * D / 2 : SS * (D - 1));
+    static constexpr int kSlot = TM * 2048;           // LDS bytes per step
+    static_assert(2 * TM % W == 0, "A copies split evenly over the waves");
+    static_assert(kWaitOdd < 64 && kWaitEven < 64, "vmcnt range");
+};
+
+template <int TM, int NG, bool BPS, bool FP4, int F>
+__global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args, int nwg,
+                                                           float* __restrict__ ws,
+                                                           const ga_splitk_ws_handle* __restrict__ wsh)
+{
+    using Cfg = LaCfg<TM, NG, BPS, FP4, F>;
+    constexpr int kEPB = FP4 ? 2 : 1;
+    constexpr int D = Cfg::D, SA = Cfg::SA, BPW = Cfg::BPW, kSlot = Cfg::kSlot;
+    constexpr bool kPair = Cfg::kPair;
+    __shared__ __attribute__((aligned(1024))) char smem[D * kSlot];
+    if (gridDim.y > 1 && wsh && !(ws = resolve_ws(wsh, gridDim.y, args.M, args.N)))
+        return; // workspace slot shorter than the split-K layout: write nothing
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int slice = blockIdx.y;
+    const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
+    const int ngroups = N / 16;
+    const int g_end = (int)(((long long)(blockIdx.x + 1) * ngroups) / nwg);
+    const int cg0 = (int)(((long long)blockIdx.x * ngroups) / nwg) + wave * NG;
+    const int ng_here = min(NG, g_end - cg0); // this wave's groups (<= 0: none)
+    const bool live = ng_here > 0;
+
+    int kpt = K;
+    if (gridDim.y > 1)
+        kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
+    const int kb = slice * kpt;
+    const int ke = min(K, kb + kpt);
+    // the same for every wave of the workgroup: all of them copy A and meet
+    // at every step's barrier, with or without columns of their own
+    const int nsteps = max(0, (ke - kb) / (128 * kEPB));
+    const int kbb = kb / kEPB, Kb = K / kEPB; // bytes
+
+    v4f acc[NG][TM];
+#pragma unroll
+    for (int c = 0; c < NG; c++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    if (nsteps > 0) {
+        const int r = lane & 15, g = lane >> 4;
+        const uint32_t lda = args.stride_A0 / kEPB; // bytes
+        const long long abytes = (long long)M * lda;
+        const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+        // A copy (i, h) of a step: lane 16g + r copies row 16i + r, K chunk
+        // g + 4h, to LDS byte lane * 16 of the copy's 1 KB; the MFMA operand
+        // of lane 16g + r is chunks g and g + 4 of row 16i + r: copies (i, 0)
+        // and (i, 1) at the same lane offset
+        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
+        __amdgpu_buffer_rsrc_t rbuf;
+        uint32_t vb, b_step, b_hi, b_grp;
+        const int ngb = live ? ng_here : 0;
+        if (BPS) {
+            const char* pb = (const char*)args.ptr_B + (size_t)(live ? cg0 : 0) * Kb * 16;
+            rbuf = make_rsrc(pb, (uint32_t)ngb * (uint32_t)Kb * 16);
+            vb = (uint32_t)lane * 16 + (uint32_t)kbb * 16;
+            b_step = 2048;
+            b_hi = 1024;
+            b_grp = (uint32_t)Kb * 16;
+        } else {
+            const uint32_t ldb = args.stride_B0 / kEPB; // bytes
+            const char* pb = (const char*)args.ptr_B + (size_t)(live ? cg0 : 0) * 16 * ldb;
+            rbuf = make_rsrc(pb, (uint32_t)ngb * 16 * ldb);
+            vb = (uint32_t)r * ldb + g * 16 + (uint32_t)kbb;
+            b_step = 128;
+            b_hi = 64;
+            b_grp = 16 * ldb;
+        }
+        const uint32_t sna = args.stride_ScaleA0, snb = args.stride_ScaleB0;
+        const auto rsa = make_rsrc(args.ptr_ScaleA, (uint32_t)((M + 31) / 32 * 32) * sna);
+        const auto rsb = make_rsrc(args.ptr_ScaleB, (uint32_t)((N + 31) / 32 * 32) * snb);
+        const uint32_t vsa = ((uint32_t)(kb / 256)) * 256 + lane * 4;
+        uint32_t vsb[NG];
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+            vsb[c] = ((uint32_t)((cg0 + c) / 2) * (snb / 8) + (uint32_t)(kb / 256)) * 256 + lane * 4;
+        const uint32_t sa_blk = (sna / 8) * 256;
+
+        v8i fb[D][NG];
+        uint32_t fsa[D][SA], fsb[D][NG];
+        uint32_t osa[TM], osb[NG];
+
+        auto copy_a = [&](int s, int slot) {
+#pragma unroll
+            for (int e = 0; e < BPW; e++) {
+                const int bi = wave * BPW + e, i = bi >> 1, h = bi & 1;
+                lds_load16(ra, (lds_void*)(smem + slot * kSlot + bi * 1024),
+                           va + uni((uint32_t)s * 128 + (uint32_t)i * 16 * lda + (uint32_t)h * 64), 0);
+            }
+        };
+        auto load_bs = [&](int s, auto J) {
+            constexpr int j = decltype(J)::value;
+            const uint32_t ob = (uint32_t)s * b_step;
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                v4i x0 = buf_load16_stream(rbuf, vb + uni(ob + c * b_grp), 0);
+                v4i x1 = buf_load16_stream(rbuf, vb + uni(ob + c * b_grp + b_hi), 0);
+                fb[j][c] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            }
+            if constexpr (!kPair || j % 2 == 0) {
+                const uint32_t q = (uint32_t)(FP4 ? s : (s >> 1)) * 256;
+#pragma unroll
+                for (int h = 0; h < SA; h++)
+                    fsa[j][h] = buf_load4(rsa, vsa + uni(q + h * sa_blk), 0);
+#pragma unroll
+                for (int c = 0; c < NG; c++)
+                    fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+            }
+        };
+        // step in slot j: A operand of rows 16i .. 16i + 15 from copies (i, 0), (i, 1)
+        v8i fa[TM];
+        auto read_a = [&](int j) {
+            const char* pa = smem + j * kSlot + lane * 16;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const v4i x0 = *(const v4i*)(pa + (2 * i) * 1024);
+                const v4i x1 = *(const v4i*)(pa + (2 * i + 1) * 1024);
+                fa[i] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            }
+        };
+        auto mma = [&](int s, auto J) {
+            constexpr int j = decltype(J)::value;
+            constexpr bool odd = kPair && j % 2 == 1;
+            const uint32_t sh = FP4 ? 0u : (uint32_t)(s & 1) * 16;
+            uint32_t sbv[NG], sav[TM];
+#pragma unroll
+            for (int c = 0; c < NG; c++)
+                sbv[c] = odd ? osb[c] : fsb[j][c] >> (sh + 8 * ((cg0 + c) & 1));
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                sav[i] = odd ? osa[i] : fsa[j][i >> 1] >> (sh + 8 * (i & 1));
+            if constexpr (kPair && j % 2 == 0) {
+#pragma unroll
+                for (int c = 0; c < NG; c++) {
+                    osb[c] = fsb[j][c] >> (16 + 8 * ((cg0 + c) & 1));
+                    asm volatile("" : "+v"(osb[c]));
+                }
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    osa[i] = fsa[j][i >> 1] >> (16 + 8 * (i & 1));
+                    asm volatile("" : "+v"(osa[i]));
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < NG; c++)
+#pragma unroll
+                for (int i = 0; i < TM; i++) {
+                    if constexpr (FP4) {
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(fb[j][c], fa[i], acc[c][i], (int)sbv[c],
+                                                        (int)sav[i]);
+                        acc[c][i] = mfma_mx16_fp4<0, 0>(hi16(fb[j][c]), hi16(fa[i]), acc[c][i],
+                                                        (int)(sbv[c] >> 16), (int)(sav[i] >> 16));
+                    } else {
+                        acc[c][i] = mfma_mx16<0, 0, fmt_of_b(F), fmt_of_a(F)>(
+                            fb[j][c], fa[i], acc[c][i], (int)sbv[c], (int)sav[i]);
+                    }
+                }
+        };
+
+        // prologue: A of steps 0 .. D-2, B and scales of steps 0 .. D-1, in
+        // step order (steps past the slice repeat its last step: every wave
+        // issues the same loads, so the counted waits hold)
+        static_for<D>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            if constexpr (j < D - 1)
+                copy_a(min(j, nsteps - 1), j);
+            load_bs(min(j, nsteps - 1), J);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        int s = 0;
+        for (; s + D <= nsteps; s += D) {
+            static_for<D>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                wait_vmcnt<(j % 2 == 0) ? Cfg::kWaitEven : Cfg::kWaitOdd>();
+                barrier_lds();
+                __builtin_amdgcn_sched_barrier(0);
+                read_a(j);
+                // the copies stay ahead of this step's B and scale loads (the
+                // waits count them in that order)
+                copy_a(min(s + j + D - 1, nsteps - 1), (j + D - 1) % D);
+                __builtin_amdgcn_sched_barrier(0);
+                mma(s + j, J);
+                load_bs(min(s + j + D, nsteps - 1), J);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        wait_vmcnt<0>();
+        barrier_lds();
+        static_for<D>([&](auto J) {
+            if ((int)J < nsteps - s) {
+                read_a(J);
+                mma(s + J, J);
+            }
+        });
+    }
+
+    if (gridDim.y > 1) {
+        if (live)
+            dec_store_partials<NG, TM>(ws, acc, slice, cg0, ng_here, M, N, lane);
+        return;
+    }
+    if (live)
+        dec_epilogue<NG, TM>(args, acc, cg0, ng_here, lane);
 }
 
 // Workgroups: one per CU (more when a CU's share needs over MAX_WAVES
@@ -461,6 +731,26 @@ void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
     case 7: launch_dec_xs<TM, (F ? 8 : 7), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
     default: launch_dec_xs<TM, 8, BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
     }
+}
+
+// Shared-A split variant: nwg workgroups per slice, each wave ceil(share / 4)
+// of its workgroup's groups (1, 2 or 4).
+template <bool BPS, bool FP4, int F>
+void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int nwg, float* ws,
+                   const ga_splitk_ws_handle* wsh, hipStream_t stream)
+{
+    const int groups = (int)args.N / 16;
+    const int share = (groups + nwg - 1) / nwg;
+    const dim3 grid(nwg, gdz);
+    if (share <= 4)
+        hipLaunchKernelGGL((mx_decode_la_kernel<4, 1, BPS, FP4, F>), grid, dim3(256), 0, stream,
+                           args, nwg, ws, wsh);
+    else if (share <= 8)
+        hipLaunchKernelGGL((mx_decode_la_kernel<4, 2, BPS, FP4, F>), grid, dim3(256), 0, stream,
+                           args, nwg, ws, wsh);
+    else
+        hipLaunchKernelGGL((mx_decode_la_kernel<4, 4, BPS, FP4, F>), grid, dim3(256), 0, stream,
+                           args, nwg, ws, wsh);
 }
 
 template <bool BPS, bool FP4, int F>
@@ -524,11 +814,29 @@ int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
 
 namespace {
 
+// Workgroups per slice of the shared-A variant: one per CU over all slices
+// (no more than the groups), at most 16 groups (4 per wave) each.
+int la_workgroups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
+{
+    const int groups = (int)args.N / 16;
+    int nwg = std::max(1, num_cu / gdz);
+    nwg = std::min(nwg, groups);
+    return std::max(nwg, (groups + 15) / 16);
+}
+
+// 33-64 rows at one slice: the shared-A variant (measured on MI355X, M = 64,
+// N = 28672, K = 8192: 45.5 us against 50-54 us for the split variant at one
+// or two slices; M = 40: 44.2 against 48.1). With more slices the split
+// variant stays (M = 64, N = 8192, K = 28672 at 4 slices: 47.6 us, shared-A
+// 51.0: the fp32 partials and the reduce cost the same, the shared-A kernel
+// streams ~7 % slower there).
 template <bool BPS, bool FP4, int F>
 void launch_split_t(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
-                    const ga_splitk_ws_handle* wsh, hipStream_t stream)
+                    const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
 {
-    if (args.M > 32)
+    if (args.M > 32 && gdz == 1 && num_cu > 0)
+        launch_dec_la<BPS, FP4, F>(args, 1, la_workgroups(args, 1, num_cu), ws, wsh, stream);
+    else if (args.M > 32)
         launch_dec_xs_ng<4, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
     else
         launch_dec_xs_ng<2, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
@@ -539,8 +847,8 @@ void launch_both(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, float* 
                  const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
 {
     if (ng > 0)
-        bps ? launch_split_t<true, FP4, F>(args, gdz, ng, ws, wsh, stream)
-            : launch_split_t<false, FP4, F>(args, gdz, ng, ws, wsh, stream);
+        bps ? launch_split_t<true, FP4, F>(args, gdz, ng, ws, wsh, num_cu, stream)
+            : launch_split_t<false, FP4, F>(args, gdz, ng, ws, wsh, num_cu, stream);
     else
         bps ? launch_dec_rows<true, FP4, F>(args, gdz, num_cu, stream)
             : launch_dec_rows<false, FP4, F>(args, gdz, num_cu, stream);
@@ -565,9 +873,10 @@ void launch_any(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4
 } // namespace
 
 void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, hipStream_t stream)
+                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, int num_cu,
+                            hipStream_t stream)
 {
-    launch_any(args, gdz, ng, bps, fp4, fmt, ws, wsh, 0, stream);
+    launch_any(args, gdz, ng, bps, fp4, fmt, ws, wsh, num_cu, stream);
 }
 
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int fmt,
