@@ -503,7 +503,7 @@ PROFILE_WORKLOADS = {
     "mxfp8_gemm_decode_16x8192x28672": ("mxd", 16, 8192, 28672, 0),
     "mxfp8_gemm_decode_1x28672x8192": ("mxd", 1, 28672, 8192, 0),
     "mxfp8_gemm_decode_1x8192x28672": ("mxd", 1, 8192, 28672, 0),
-    "mxfp8_gemm_decode_64x28672x8192": ("mxd", 64, 28672, 8192, 1),
+    "mxfp8_gemm_decode_64x28672x8192": ("mxd", 64, 28672, 8192, 0),
     "mxfp8_gemm_decode_64x8192x28672": ("mxd", 64, 8192, 28672, 2),
     "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out": ("bs", 8192, 8192, 8192, 0),
     "fp8_per_tensor_8192x8192x8192_bf16out": ("pt", 8192, 8192, 8192, 0),
