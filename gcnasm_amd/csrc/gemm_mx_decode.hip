@@ -733,8 +733,8 @@ void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
     }
 }
 
-// Shared-A split variant: nwg workgroups per slice, each wave ceil(share / 4)
-// of its workgroup's groups (1, 2 or 4).
+// Shared-A split variant: nwg workgroups per slice, each wave up to 2 (a
+// share of at most 8 groups) or 4 of its workgroup's groups.
 template <bool BPS, bool FP4, int F>
 void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int nwg, float* ws,
                    const ga_splitk_ws_handle* wsh, hipStream_t stream)
@@ -742,10 +742,7 @@ void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int nwg, float* ws,
     const int groups = (int)args.N / 16;
     const int share = (groups + nwg - 1) / nwg;
     const dim3 grid(nwg, gdz);
-    if (share <= 4)
-        hipLaunchKernelGGL((mx_decode_la_kernel<4, 1, BPS, FP4, F>), grid, dim3(256), 0, stream,
-                           args, nwg, ws, wsh);
-    else if (share <= 8)
+    if (share <= 8)
         hipLaunchKernelGGL((mx_decode_la_kernel<4, 2, BPS, FP4, F>), grid, dim3(256), 0, stream,
                            args, nwg, ws, wsh);
     else

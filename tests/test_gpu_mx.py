@@ -344,6 +344,30 @@ def test_decode_split_across_workgroups(dev, M, bps, NKL):
           ("bps" if bps else "plain", M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
+# 33-64 rows at one slice over wide N: the shared-A variant (four waves per
+# workgroup, A through an LDS ring). (M, N, K, preshuffled B): 2 groups per
+# wave with the ring (8 steps) longer than the slice (5 steps), 33 rows; 9
+# steps (one pass of the main loop and a one-step tail), waves of 2, 2, 1 and
+# no groups; 4 groups per wave (N > 32768: the five-step ring without paired
+# scale loads) over 13 steps (two passes, a three-step tail) and 9, with one
+# workgroup of 9 groups among 8s.
+SHARED_A_CASES = [(33, 24576, 640, True), (33, 24576, 640, False), (40, 20480, 1152, True),
+                  (64, 32784, 1664, True), (64, 32784, 1152, False)]
+
+
+@pytest.mark.parametrize("MNKB", SHARED_A_CASES)
+def test_decode_shared_a(dev, MNKB):
+    M, N, K, bps = MNKB
+    name = ("ga_mxfp8_bf16_BpreShuffle_256x256" if bps else
+            "ga_mxfp8_bf16_noBpreShuffle_256x256")
+    cfg = cfg_named(name)
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=5 * M + K, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, 0)
+    assert ld.gdz == 1
+    check(got, expect(qa, sa, qb, sb, 0), "decode shared-A %s M=%d N=%d K=%d" %
+          ("bps" if bps else "plain", M, N, K), oracle.mx_absdot(qa, sa, qb, sb))
+
+
 def test_decode_split_epilogue(dev):
     """alpha/beta through the split variant (applied by the split-K reduce)."""
     M, N, K, l2 = 40, 512, 2048, 2

@@ -247,6 +247,21 @@ def test_fp4_decode_split_across_workgroups(dev, M, bps, NKL):
     check4(got, qa, sa, qb, sb, l2, "decode split %s M=%d" % (name, M))
 
 
+@pytest.mark.parametrize("MNKB", [(64, 32784, 1792, True), (40, 20480, 2304, False),
+                                  (33, 24576, 1280, True)])
+def test_fp4_decode_shared_a(dev, MNKB):
+    """33-64 rows at one slice over wide N: the shared-A variant with 4 groups
+    per wave (N > 32768; 7 steps: a five-step ring and a two-step tail) and 2
+    (9 steps against a seven-step ring; 5 steps, shorter than the ring),
+    MXFP4 operands (one scale dword per step)."""
+    M, N, K, bps = MNKB
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + K)
+    name = ("ga_mxfp4_bf16_BpreShuffle_256x256" if bps else
+            "ga_mxfp4_bf16_noBpreShuffle_256x256")
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4(name), 0)
+    check4(got, qa, sa, qb, sb, 0, "decode shared-A %s M=%d N=%d K=%d" % (name, M, N, K))
+
+
 def test_fp4_k_not_multiple_of_256_is_rejected(dev):
     M, N, K = 64, 256, 384
     sh = f4gemm.Shape(M, N, K, elem_bits=4)
