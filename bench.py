@@ -27,8 +27,11 @@ e2m1, DeepSeek 1x128 and 128x128) on an 8192x8192 fp32 and bf16 input.
 
 "blockscale" times the DeepSeek-style GEMM (1x128 activation / 128x128 weight
 fp32 scales, fp32 C, opus_gemm kargs) at 8192^3 next to the reference's own
-published number for it (opus_gemm/block_scale_gemm/README.md:114), and the
-per-tensor fp8_gemm at 8192^3 (bf16 C).
+published number for it (opus_gemm/block_scale_gemm/README.md:114), on N(0,1)
+data and on the reference driver's distribution ("refdata"), the other sizes
+of that published table (1024^3 to 16384^3, README.md:111-115) on the
+driver's distribution ("reference_table"), and the per-tensor fp8_gemm at
+8192^3 (bf16 C).
 
 "a16w16_splitk" times the bf16 split-K GEMM + reduce (the reference's
 opus_gemm_mem_gemm_a2a driver, without its all-to-all) at the driver's default
@@ -449,13 +452,7 @@ def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
     pt["frac_fp8_peak"] = pt["roofline"]["frac"]
     del xa, xb, qa, qb, cb
     # the reference driver's distribution
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(7)
-    ra = torch.rand((n, n), device="cuda:0", generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
-    rb = (torch.rand((n, n), device="cuda:0", generator=g) - 0.5).to(
-        torch.float8_e4m3fn).view(torch.uint8)
-    rsfa = torch.rand((n // 128, n), device="cuda:0", generator=g) * 0.4 + 0.8
-    rsfb = torch.rand((n // 128, n // 128), device="cuda:0", generator=g) * 0.4 + 0.8
+    ra, rb, rsfa, rsfb = ref_bs_operands(torch, n, 7)
     us = time_opus(torch, opus_gemm, ra, rb, rsfa, rsfb, c, 128, steps, warmup)
     bsr = opus_leg("fp8_blockscale_1x128_128x128_8192x8192x8192_f32out_refdata", n, n, n, us,
                    {"data": "the reference driver's: A~U[0,1) B~U[-.5,.5) as E4M3, "
@@ -465,7 +462,46 @@ def fp32_scaled_gemms(torch, ops, opus_gemm, steps, warmup):
     bs["refdata"] = bsr
     del ra, rb, rsfa, rsfb, c
     torch.cuda.empty_cache()
+    bs["reference_table"] = blockscale_reference_table(torch, opus_gemm, steps, warmup)
     return bs, pt
+
+
+def ref_bs_operands(torch, n, seed):
+    """n x n block-scale operands in the reference driver's distribution
+    (gemm_a8w8_blockscale_host.cc:207-210): A ~ U[0,1), B ~ U[-0.5,0.5) as
+    E4M3, SFA [n/128, n] and SFB [n/128, n/128] ~ U[0.8,1.2)."""
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(seed)
+    ra = torch.rand((n, n), device="cuda:0", generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    rb = (torch.rand((n, n), device="cuda:0", generator=g) - 0.5).to(
+        torch.float8_e4m3fn).view(torch.uint8)
+    rsfa = torch.rand((n // 128, n), device="cuda:0", generator=g) * 0.4 + 0.8
+    rsfb = torch.rand((n // 128, n // 128), device="cuda:0", generator=g) * 0.4 + 0.8
+    return ra, rb, rsfa, rsfb
+
+
+# The reference's published block-scale table (1x128 / 128x128 fp32 scales,
+# fp32 C, M = N = K), milliseconds on MI355X: opus_gemm/block_scale_gemm/
+# README.md:111-115 (8192 is the refdata entry above).
+REF_BLOCKSCALE_TABLE_MS = ((1024, 0.0181), (2048, 0.0279), (4096, 0.0614), (16384, 3.2737))
+
+
+def blockscale_reference_table(torch, opus_gemm, steps, warmup):
+    """The block-scale GEMM at the reference's other published sizes, on its
+    driver's operand distribution, against its published times."""
+    table = []
+    for n, ref_ms in REF_BLOCKSCALE_TABLE_MS:
+        ra, rb, rsfa, rsfb = ref_bs_operands(torch, n, 7 + n)
+        c = torch.empty((n, n), dtype=torch.float32, device="cuda:0")
+        calls = max(steps, 100) if n <= 4096 else steps
+        us = time_opus(torch, opus_gemm, ra, rb, rsfa, rsfb, c, 128, calls, warmup)
+        fl = 2.0 * n * n * n
+        table.append({"shape": [n, n, n], "kernel_avg_us": round(us, 2),
+                      "tflops": round(fl / us / 1e6, 1), "reference_us": ref_ms * 1e3,
+                      "vs_reference": round(ref_ms * 1e3 / us, 4)})
+        del ra, rb, rsfa, rsfb, c
+        torch.cuda.empty_cache()
+    return table
 
 
 DEEPSEEK_SHAPES = ((4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536))
