@@ -168,6 +168,46 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ 
 // ---- DeepSeek 1x128 -----------------------------------------------------------
 __device__ __forceinline__ float ds_scale(float amax) { return amax > 0.0f ? amax / 448.0f : 1.0f; }
 
+// x / s for the elements that share one scale s, exact wherever the quotient
+// decides an E4M3 code. For finite s >= 2^-64: the reciprocal r = 1/s
+// (correctly rounded, once per scale), q0 = x*r, and two corrections
+// q <- q + (x - q*s)*r, each residual and product one FMA. With r within
+// half an ulp of 1/s and q within one ulp of x/s, the corrected quotient is
+// x/s correctly rounded (Markstein's theorem; the first correction brings
+// q0, within 1.5 ulp, inside one ulp). The residuals stay normal numbers for
+// every x whose quotient is at least 2^-12 (|x| >= 2^-76), the range in which
+// the fp32 quotient can change an E4M3 code; smaller quotients come out
+// below 2^-11 with x's sign, and such values encode to the signed zero either
+// way. The sign is taken from x, so -0 stays -0. tests/scale_div_check.c
+// restates this arithmetic on the CPU and compares it with IEEE division
+// (every bf16 x and random fp32 x under scales over the whole range; 1.4e9
+// quotients without a mismatch). Other scales (subnormal, infinite) divide. Five VALU instructions per element instead
+// of the IEEE division's ten; the choice is made once per scale.
+struct ScaleDiv {
+    float s, r;
+    bool fast;
+    __device__ __forceinline__ explicit ScaleDiv(float s_)
+        : s(s_), r(1.0f / s_), fast(s_ >= 0x1p-64f && s_ <= 3.40282347e38f)
+    {
+    }
+    template <int N>
+    __device__ __forceinline__ void div(const float (&v)[N], float (&t)[N]) const
+    {
+        if (fast) {
+#pragma unroll
+            for (int j = 0; j < N; j++) {
+                const float q0 = v[j] * r;
+                const float q1 = fmaf(fmaf(-q0, s, v[j]), r, q0);
+                t[j] = copysignf(fmaf(fmaf(-q1, s, v[j]), r, q1), v[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; j++)
+                t[j] = v[j] / s;
+        }
+    }
+};
+
 // A 1x128 group is LPB = 128/EPL lanes; U groups per lane as above.
 template <int IN, int EPL, int U>
 __global__ __launch_bounds__(256) void quant_1x128_kernel(const void* __restrict__ x, int rows,
@@ -198,9 +238,7 @@ __global__ __launch_bounds__(256) void quant_1x128_kernel(const void* __restrict
             continue;
         const float sc = ds_scale(amax);
         float t[EPL];
-#pragma unroll
-        for (int j = 0; j < EPL; j++)
-            t[j] = v[u][j] / sc;
+        ScaleDiv(sc).div(v[u], t);
         uint8_t* dst = q + (size_t)rr[u] * ld_q + gg[u] * 128 + sub * EPL;
         if constexpr (EPL == 8) {
             uint2 w;
@@ -248,15 +286,14 @@ __global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restri
     __syncthreads();
     amax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
     const float sc = ds_scale(__uint_as_float(amax));
+    const ScaleDiv d(sc);
 #pragma unroll
     for (int i = 0; i < NP; i++) {
         const int r = rb * 128 + r_lo + i * RPP;
         if (r >= rows)
             continue;
         float t[EPL];
-#pragma unroll
-        for (int j = 0; j < EPL; j++)
-            t[j] = v[i][j] / sc;
+        d.div(v[i], t);
         uint8_t* dst = q + (size_t)r * ld_q + g * 128 + col;
         if constexpr (EPL == 8) {
             uint2 w;
@@ -314,6 +351,7 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const void* __restric
                                                            float* __restrict__ scale)
 {
     const float sc = ds_scale(__uint_as_float(*amax_bits));
+    const ScaleDiv d(sc);
     if (blockIdx.x == 0 && threadIdx.x == 0)
         *scale = sc;
     const size_t n4 = n / 4;
@@ -328,15 +366,20 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const void* __restric
 #pragma unroll
         for (int u = 0; u < kTensorU; u++) {
             const size_t i = i0 + u * stride;
-            if (i < n4)
-                *(uint32_t*)(q + i * 4) = e4m3_encode4(v[u][0] / sc, v[u][1] / sc, v[u][2] / sc,
-                                                       v[u][3] / sc);
+            if (i < n4) {
+                float t[4];
+                d.div(v[u], t);
+                *(uint32_t*)(q + i * 4) = e4m3_encode4(t[0], t[1], t[2], t[3]);
+            }
         }
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         size_t i = n4 * 4 + threadIdx.x;
         float v = IN == GA_IN_F32 ? ((const float*)x)[i] : bf16_to_f32(((const uint16_t*)x)[i]);
-        q[i] = (uint8_t)e4m3_encode(v / sc);
+        const float vv[1] = {v};
+        float t[1];
+        d.div(vv, t);
+        q[i] = (uint8_t)e4m3_encode(t[0]);
     }
 }
 
@@ -407,7 +450,12 @@ using namespace ga;
             hipLaunchKernelGGL(KERNEL<GA_IN_BF16>, __VA_ARGS__);                   \
     } while (0)
 
-constexpr int kQU = 4; // 1x32 / 1x128 blocks per lane
+// 1x32 / 1x128 blocks per lane: two for fp32 and 8-byte bf16 loads, one for
+// 16-byte bf16 loads (16-32 bytes in flight per lane). Measured on MI355X at
+// 8192x8192 (fraction of 8 TB/s, 4 blocks -> this): MX E4M3 fp32 0.70 -> 0.73,
+// bf16 0.62 -> 0.71; e2m1 bf16 0.55 -> 0.63; 1x128 bf16 0.46 -> 0.51.
+constexpr int kQU = 2;
+constexpr int kQUWide = 1;
 
 // bf16 inputs use 16-byte loads (8 elements per lane) when the row stride and
 // base allow it and the codes' stores stay aligned (store_align: bytes per
@@ -425,13 +473,14 @@ static void launch_quant_mx(int in_dtype, bool wide, long long blocks, hipStream
                             uint8_t* s, int ld_s, int rule)
 {
     const int epl = in_dtype == GA_IN_F32 ? 4 : (wide ? 8 : 4);
-    const unsigned grid = grid1d(blocks, (256 / (32 / epl)) * kQU);
+    const int u = (in_dtype != GA_IN_F32 && wide) ? kQUWide : kQU;
+    const unsigned grid = grid1d(blocks, (256 / (32 / epl)) * u);
     if (in_dtype == GA_IN_F32)
         hipLaunchKernelGGL((quant_mx_kernel<GA_IN_F32, 4, FP4, kQU, E5>), dim3(grid), dim3(256), 0,
                            st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
     else if (wide)
-        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 8, FP4, kQU, E5>), dim3(grid), dim3(256),
-                           0, st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
+        hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 8, FP4, kQUWide, E5>), dim3(grid),
+                           dim3(256), 0, st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
     else
         hipLaunchKernelGGL((quant_mx_kernel<GA_IN_BF16, 4, FP4, kQU, E5>), dim3(grid), dim3(256),
                            0, st, x, rows, K, ld_x, q, ld_q, s, ld_s, rule);
@@ -507,8 +556,8 @@ ga_status ga_quant_fp8_1x128(const void* x, int in_dtype, int rows, int K, int l
         hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_F32, 4, kQU>), dim3(grid1d(blocks, 8 * kQU)),
                            dim3(256), 0, st, x, rows, K, ld_x, (uint8_t*)q, ld_q, sfa, ld_s);
     else if (bf16_wide(in_dtype, x, ld_x, q, ld_q, 8))
-        hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_BF16, 8, kQU>),
-                           dim3(grid1d(blocks, 16 * kQU)), dim3(256), 0, st, x, rows, K, ld_x,
+        hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_BF16, 8, kQUWide>),
+                           dim3(grid1d(blocks, 16 * kQUWide)), dim3(256), 0, st, x, rows, K, ld_x,
                            (uint8_t*)q, ld_q, sfa, ld_s);
     else
         hipLaunchKernelGGL((quant_1x128_kernel<GA_IN_BF16, 4, kQU>), dim3(grid1d(blocks, 8 * kQU)),

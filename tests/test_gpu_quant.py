@@ -129,6 +129,44 @@ def test_e4m3_encoder_every_bf16_value(dev):
         np.testing.assert_array_equal(q.cpu().numpy(), oracle.e4m3_encode(x))
 
 
+@pytest.mark.parametrize("amax", [1000.5, 3.7e-5, 1.7 * 2.0 ** -50, 2.0 ** -60, 3.0e38])
+def test_quant_division_every_bf16_value(dev, amax):
+    """The 1x128, 128x128 and per-tensor quantisers divide by s = amax/448,
+    which is not a power of two: blocks whose first element is the maximum
+    and whose other elements run through every bf16 value of magnitude <=
+    amax (both signs, zeros included), at scales on both sides of the 2^-64
+    bound of the shared-reciprocal division (1.7 * 2^-50 / 448 above it,
+    2^-60 / 448 below), checked bit for bit against the oracle's fp32 division
+    for fp32 and bf16 input."""
+    top = oracle.bf16_bits_to_f32(oracle.to_bf16_bits(np.array([amax], np.float32)))[0]
+    allv = oracle.bf16_bits_to_f32(np.arange(0x7F80, dtype=np.uint32).astype(np.uint16))
+    vals = allv[allv <= top]
+    vals = np.concatenate([vals, -vals]).astype(np.float32)
+    nblk = -(-len(vals) // 127)
+    nblk = -(-nblk // 8) * 8  # whole rows of K = 1024
+    body = np.zeros(nblk * 127, np.float32)
+    body[:len(vals)] = vals
+    x = np.concatenate([np.full((nblk, 1), top, np.float32), body.reshape(nblk, 127)], axis=1)
+    x = np.ascontiguousarray(x.reshape(-1, 1024))
+    xb = oracle.to_bf16_bits(x)
+    assert np.array_equal(oracle.bf16_bits_to_f32(xb), x)
+    o1, os1 = oracle.quant_fp8_1x128(x)
+    o2, os2 = oracle.quant_fp8_128x128(x)
+    o3, os3 = oracle.quant_fp8_per_tensor(x)
+    for t in (torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16),
+              torch.from_numpy(x).to(dev)):
+        q1, s1 = ops.quant_fp8_1x128(t)
+        q2, s2 = ops.quant_fp8_128x128(t)
+        q3, s3 = ops.quant_fp8_per_tensor(t)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(s1.cpu().numpy().view(np.uint32), os1.view(np.uint32))
+        np.testing.assert_array_equal(q1.cpu().numpy(), o1)
+        np.testing.assert_array_equal(s2.cpu().numpy().view(np.uint32), os2.view(np.uint32))
+        np.testing.assert_array_equal(q2.cpu().numpy(), o2)
+        np.testing.assert_array_equal(s3.cpu().numpy().view(np.uint32), os3.view(np.uint32))
+        np.testing.assert_array_equal(q3.cpu().numpy(), o3)
+
+
 @pytest.mark.parametrize("NK", [(16, 32), (256, 512), (272, 4096)])
 def test_device_shuffle_weight(dev, NK):
     N, Kp = NK

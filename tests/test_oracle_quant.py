@@ -174,3 +174,19 @@ def test_mx_e5m2_floor_rule_saturates_block_max():
             blk = x[r, b * 32:(b + 1) * 32]
             i = int(np.argmax(np.abs(blk)))
             assert q[r, b * 32 + i] & 0x7F == 0x7B
+
+
+def test_shared_scale_division_is_exact(tmp_path):
+    """The 1x128 / 128x128 / per-tensor quantisers divide by a block scale
+    with a shared reciprocal and two FMA corrections (quant.hip, ScaleDiv):
+    scale_div_check.c restates that arithmetic on the CPU and compares it with
+    IEEE division for every bf16 value and random fp32 values under 300
+    scales (~1.5e7 quotients)."""
+    import os
+    import subprocess
+    src = os.path.join(os.path.dirname(__file__), "scale_div_check.c")
+    exe = str(tmp_path / "scale_div_check")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, src, "-lm"], check=True)
+    out = subprocess.run([exe, "300"], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stdout
+    assert " 0 mismatches" in out.stdout
