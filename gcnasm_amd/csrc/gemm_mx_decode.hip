@@ -442,7 +442,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
 // step, the odd step's operands shifted out during the even step.
 // One slice applies the epilogue; more write fp32 partials for the split-K
 // reduce (ws, or the slot wsh), as the split variant does.
-template <int TM, int NG, bool BPS, bool FP4, int F>
+template <int TM, int NG, bool FP4>
 struct LaCfg {
     static constexpr int W = 4;                       // waves per workgroup
     static constexpr int SA = (TM + 1) / 2;           // A scale dwords per step
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
                                                            float* __restrict__ ws,
                                                            const ga_splitk_ws_handle* __restrict__ wsh)
 {
-    using Cfg = LaCfg<TM, NG, BPS, FP4, F>;
+    using Cfg = LaCfg<TM, NG, FP4>;
     constexpr int kEPB = FP4 ? 2 : 1;
     constexpr int D = Cfg::D, SA = Cfg::SA, BPW = Cfg::BPW, kSlot = Cfg::kSlot;
     constexpr bool kPair = Cfg::kPair;
