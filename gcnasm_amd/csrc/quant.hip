@@ -96,6 +96,33 @@ __device__ __forceinline__ uint32_t group_max_dpp(uint32_t a)
     return a;
 }
 
+// Maximum of the plain keys bits & 0x7FFFFFFF: one instruction per element
+// instead of abs_key's three. A NaN's key is above +inf's, so a maximum above
+// 0x7F800000 means the block holds a NaN; only then (rare) is the
+// NaN-ignoring maximum taken.
+template <int EPL>
+__device__ __forceinline__ uint32_t amax_raw(const float (&v)[EPL])
+{
+    uint32_t a = __float_as_uint(v[0]) & 0x7FFFFFFFu;
+#pragma unroll
+    for (int j = 1; j < EPL; j++)
+        a = max(a, __float_as_uint(v[j]) & 0x7FFFFFFFu);
+    return a;
+}
+
+// The NaN-ignoring maximum of |x| over aligned groups of W lanes. The
+// recomputation is taken by the whole wave when any of its blocks holds a
+// NaN (a ballot makes the branch uniform), so the lane exchanges always run
+// with every lane active.
+template <int W, int EPL>
+__device__ __forceinline__ uint32_t block_amax(const float (&v)[EPL])
+{
+    uint32_t a = group_max_dpp<W>(amax_raw<EPL>(v));
+    if (__builtin_amdgcn_ballot_w64(a > 0x7F800000u) != 0)
+        a = group_max_dpp<W>(amax_n<EPL>(v));
+    return a;
+}
+
 // ---- MX 1x32 (E4M3 or packed e2m1 codes) -------------------------------------
 // A 1x32 block is LPB = 32/EPL lanes of EPL elements (16-byte loads where the
 // layout allows); each lane handles U blocks, BPP = 256/LPB blocks apart, so U
@@ -125,7 +152,7 @@ __global__ __launch_bounds__(256) void quant_mx_kernel(const void* __restrict__ 
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const float amax = __uint_as_float(group_max_dpp<LPB>(amax_n<EPL>(v[u])));
+        const float amax = __uint_as_float(block_amax<LPB, EPL>(v[u]));
         if (!ok[u])
             continue;
         const int e = FP4 ? mx4_scale_exp(amax, rule)
@@ -233,7 +260,7 @@ __global__ __launch_bounds__(256) void quant_1x128_kernel(const void* __restrict
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const float amax = __uint_as_float(group_max_dpp<LPB>(amax_n<EPL>(v[u])));
+        const float amax = __uint_as_float(block_amax<LPB, EPL>(v[u]));
         if (!ok[u])
             continue;
         const float sc = ds_scale(amax);
@@ -276,15 +303,25 @@ __global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restri
         const int r = rb * 128 + r_lo + i * RPP;
         load_elems<IN, EPL>(x, (size_t)r * ld_x + g * 128 + col, r < rows, v[i]);
     }
+    // the tile's maximum over the plain keys; only a tile holding a NaN
+    // (the maximum says so, the same in every wave) takes the NaN-ignoring one
+    auto tile_max = [&](bool nan_free) {
+        uint32_t a = 0u;
 #pragma unroll
-    for (int i = 0; i < NP; i++)
-        amax = max(amax, amax_n<EPL>(v[i]));
-    amax = group_max_dpp<32>(amax);
-    amax = max(amax, (uint32_t)__shfl_xor((int)amax, 32, 64));
-    if ((tid & 63) == 0)
-        wmax[tid >> 6] = amax;
-    __syncthreads();
-    amax = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+        for (int i = 0; i < NP; i++)
+            a = max(a, nan_free ? amax_n<EPL>(v[i]) : amax_raw<EPL>(v[i]));
+        a = group_max_dpp<32>(a);
+        a = max(a, (uint32_t)__shfl_xor((int)a, 32, 64));
+        if ((tid & 63) == 0)
+            wmax[tid >> 6] = a;
+        __syncthreads();
+        return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+    };
+    amax = tile_max(false);
+    if (amax > 0x7F800000u) {
+        __syncthreads(); // every wave has read wmax before it is written again
+        amax = tile_max(true);
+    }
     const float sc = ds_scale(__uint_as_float(amax));
     const ScaleDiv d(sc);
 #pragma unroll

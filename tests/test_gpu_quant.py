@@ -129,6 +129,51 @@ def test_e4m3_encoder_every_bf16_value(dev):
         np.testing.assert_array_equal(q.cpu().numpy(), oracle.e4m3_encode(x))
 
 
+@pytest.mark.parametrize("in_bf16", [False, True])
+def test_quant_nan_blocks(dev, in_bf16):
+    """Block maxima ignore NaNs (the CPU reference's `a > amax` scan): NaNs,
+    quiet, signalling and negative, as the first or last element of a 1x32
+    block, next to the block's largest value, filling a whole 1x32 / 1x128
+    block, and in one 128x128 tile only, among blocks without NaNs in the same
+    wave; every quantiser against the oracle, codes and scales."""
+    rows, K = 256, 1024
+    x = oracle.gen_mx_input(rows, K, 91, 1.0, 6)
+    nans = np.array([0x7FC00000, 0x7F800001, 0xFFC00000, 0xFFBFFFFF], np.uint32).view(np.float32)
+    x[0, 0] = nans[0]                  # first of its 1x32 block
+    x[1, 31] = nans[1]                 # last of its block (signalling)
+    x[2, 40] = nans[2]                 # negative
+    x[2, 41] = 300.0                   # beside the block's maximum
+    x[3, 64:96] = nans[3]              # a whole 1x32 block
+    x[4, 128:256] = nans[0]            # a whole 1x128 block
+    x[200, 900] = nans[1]              # one NaN in tile (1, 7)
+    if in_bf16:
+        xb = oracle.to_bf16_bits(x)
+        x = oracle.bf16_bits_to_f32(xb)
+        xt = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    assert np.isnan(x).sum() == 3 + 32 + 128 + 1
+    for rule in (0, 1, 2):
+        q, sc = ops.quant_mxfp8(xt, rule)
+        q4, s4 = ops.quant_mxfp4(xt, rule)
+        torch.cuda.synchronize()
+        qo, so = oracle.quant_mxfp8(x, rule)
+        np.testing.assert_array_equal(sc.cpu().numpy(), so)
+        np.testing.assert_array_equal(q.cpu().numpy(), qo)
+        q4o, s4o = oracle.quant_mxfp4(x, rule)
+        np.testing.assert_array_equal(s4.cpu().numpy(), s4o)
+        np.testing.assert_array_equal(q4.cpu().numpy(), q4o)
+    q1, s1 = ops.quant_fp8_1x128(xt)
+    q2, s2 = ops.quant_fp8_128x128(xt)
+    torch.cuda.synchronize()
+    o1, os1 = oracle.quant_fp8_1x128(x)
+    o2, os2 = oracle.quant_fp8_128x128(x)
+    np.testing.assert_array_equal(s1.cpu().numpy().view(np.uint32), os1.view(np.uint32))
+    np.testing.assert_array_equal(q1.cpu().numpy(), o1)
+    np.testing.assert_array_equal(s2.cpu().numpy().view(np.uint32), os2.view(np.uint32))
+    np.testing.assert_array_equal(q2.cpu().numpy(), o2)
+
+
 @pytest.mark.parametrize("amax", [1000.5, 3.7e-5, 1.7 * 2.0 ** -50, 2.0 ** -60, 3.0e38])
 def test_quant_division_every_bf16_value(dev, amax):
     """The 1x128, 128x128 and per-tensor quantisers divide by s = amax/448,
