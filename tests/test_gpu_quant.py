@@ -10,7 +10,8 @@ pytestmark = pytest.mark.gpu
 
 
 def edge_values():
-    """Ties, subnormal boundaries, saturation, zeros of both signs, inf/NaN."""
+    """Ties, subnormal boundaries, saturation, zeros of both signs, infinities
+    (NaNs: test_quant_nan_blocks)."""
     vals = [0.0, -0.0, 448.0, -448.0, 464.0, 480.0, 1e30, -1e30, np.inf, -np.inf,
             2.0 ** -6, 2.0 ** -7, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -10, 1.0625, 1.1875,
             1.0 + 2.0 ** -4, 1.0 + 3 * 2.0 ** -4, 3.0e-45]
