@@ -921,17 +921,18 @@ def main():
         del a, bs
         torch.cuda.empty_cache()
     if "mxfp4_decode" in legs:
-        extra["mxfp4_decode"] = mxfp4_decode_leg(torch, ops, f4gemm, 20, 5)
+        extra["mxfp4_decode"] = mxfp4_decode_leg(torch, ops, f4gemm, args.steps, args.warmup)
     if "quant" in legs:
-        extra["quantisers"] = quant_legs(torch, 20, 5)
+        extra["quantisers"] = quant_legs(torch, args.steps, args.warmup)
     if "blockscale" in legs:
-        extra["blockscale"], extra["per_tensor"] = fp32_scaled_gemms(torch, ops, opus_gemm, 20, 5)
+        extra["blockscale"], extra["per_tensor"] = fp32_scaled_gemms(torch, ops, opus_gemm,
+                                                                     args.steps, args.warmup)
     if "deepseek" in legs:
-        extra["deepseek"] = deepseek_legs(torch, ops, opus_gemm, 30, 5)
+        extra["deepseek"] = deepseek_legs(torch, ops, opus_gemm, args.steps, args.warmup)
     if "mxfp4" in legs:
-        extra["mxfp4"] = mxfp4_leg(torch, ops, f4gemm, 20, 5)
+        extra["mxfp4"] = mxfp4_leg(torch, ops, f4gemm, args.steps, args.warmup)
     if "a16w16" in legs:
-        extra["a16w16_splitk"] = a16w16_leg(torch, 50, 10)
+        extra["a16w16_splitk"] = a16w16_leg(torch, args.steps, args.warmup)
 
     out = {
         "metric": "MXFP8 GEMM TFLOP/s & % FP8 MFMA peak at 8192^3; HBM GB/s at M=16 decode",
