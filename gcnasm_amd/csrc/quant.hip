@@ -281,18 +281,21 @@ __global__ __launch_bounds__(256) void quant_1x128_kernel(const void* __restrict
 }
 
 // ---- DeepSeek 128x128: one workgroup per tile ----------------------------------
-// The tile is read once into registers (64 values per lane: 16 / 8 loads in
-// flight), reduced in the workgroup, then quantised from registers.
+// The tile is read once into registers (32 values per lane with 512 threads:
+// 8 / 4 loads in flight for fp32 / bf16), reduced in the workgroup, then
+// quantised from registers. Measured on MI355X at 8192x8192 against 256
+// threads (fraction of 8 TB/s): fp32 0.72-0.73 -> 0.78, bf16 0.63 -> 0.72.
+constexpr int kTileThreads = 512;
+
 template <int IN, int EPL>
-__global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restrict__ x, int rows,
-                                                            int K, int ld_x,
-                                                            uint8_t* __restrict__ q, int ld_q,
-                                                            float* __restrict__ sfb, int ld_s)
+__global__ __launch_bounds__(kTileThreads) void quant_128x128_kernel(
+    const void* __restrict__ x, int rows, int K, int ld_x, uint8_t* __restrict__ q, int ld_q,
+    float* __restrict__ sfb, int ld_s)
 {
-    constexpr int LPR = 128 / EPL;     // lanes per tile row
-    constexpr int RPP = 256 / LPR;     // rows per pass
-    constexpr int NP = 128 / RPP;      // passes
-    __shared__ uint32_t wmax[4];
+    constexpr int LPR = 128 / EPL;          // lanes per tile row
+    constexpr int RPP = kTileThreads / LPR; // rows per pass
+    constexpr int NP = 128 / RPP;           // passes
+    __shared__ uint32_t wmax[kTileThreads / 64];
     const int g = blockIdx.x, rb = blockIdx.y;
     const int tid = threadIdx.x;
     const int col = (tid % LPR) * EPL, r_lo = tid / LPR;
@@ -315,7 +318,11 @@ __global__ __launch_bounds__(256) void quant_128x128_kernel(const void* __restri
         if ((tid & 63) == 0)
             wmax[tid >> 6] = a;
         __syncthreads();
-        return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+        uint32_t m = wmax[0];
+#pragma unroll
+        for (int w = 1; w < kTileThreads / 64; w++)
+            m = max(m, wmax[w]);
+        return m;
     };
     amax = tile_max(false);
     if (amax > 0x7F800000u) {
@@ -615,13 +622,13 @@ ga_status ga_quant_fp8_128x128(const void* x, int in_dtype, int rows, int K, int
     dim3 grid(K / 128, (rows + 127) / 128);
     hipStream_t st = (hipStream_t)stream;
     if (in_dtype == GA_IN_F32)
-        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_F32, 4>), grid, dim3(256), 0, st, x, rows,
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_F32, 4>), grid, dim3(kTileThreads), 0, st, x, rows,
                            K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
     else if (bf16_wide(in_dtype, x, ld_x, q, ld_q, 8))
-        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 8>), grid, dim3(256), 0, st, x, rows,
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 8>), grid, dim3(kTileThreads), 0, st, x, rows,
                            K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
     else
-        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 4>), grid, dim3(256), 0, st, x, rows,
+        hipLaunchKernelGGL((quant_128x128_kernel<GA_IN_BF16, 4>), grid, dim3(kTileThreads), 0, st, x, rows,
                            K, ld_x, (uint8_t*)q, ld_q, sfb, ld_s);
     GA_HIP_CHECK(hipGetLastError());
     return GA_OK;
