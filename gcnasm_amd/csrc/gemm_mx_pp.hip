@@ -192,7 +192,9 @@ struct PpArgs {
 // step reads one whole shuffled scale dword per 32-row block.
 // Two quadrants with shared A fragments: acc0 += A x B0, acc1 += A x B1
 // (16 MFMAs at raised issue priority).
-template <bool FP4, int F>
+// MXFP8 with whole scale dwords: SB = 2 * (128-K half) selects the step's
+// bytes in the operand (0 when the step's two bytes were read into 0-15).
+template <bool FP4, int F, int SB = 0>
 __device__ __forceinline__ void mma_two(v4f (&acc0)[4][2], v4f (&acc1)[4][2], const v8i (&a)[4],
                                         const v8i (&b0)[2], const v8i (&b1)[2],
                                         const uint32_t (&sa)[2], uint32_t sb0, uint32_t sb1)
@@ -209,7 +211,7 @@ __device__ __forceinline__ void mma_two(v4f (&acc0)[4][2], v4f (&acc1)[4][2], co
                     acc[i][t] = mfma_mx16_fp4<2 + (t & 1), 2 + (i & 1)>(
                         hi16(b[t]), hi16(a[i]), acc[i][t], (int)sb, (int)sa[i >> 1]);
                 } else {
-                    acc[i][t] = mfma_mx16<(t & 1), (i & 1), fmt_of_b(F), fmt_of_a(F)>(
+                    acc[i][t] = mfma_mx16<SB + (t & 1), SB + (i & 1), fmt_of_b(F), fmt_of_a(F)>(
                         b[t], a[i], acc[i][t], (int)sb, (int)sa[i >> 1]);
                 }
             });
@@ -382,6 +384,49 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
         // MXFP4: both halves of the scales of step s + 2, into ring slot
         // (s + 2) % 3 (that of step s - 1).
         int r0 = 0; // scale ring slot of step s (MXFP8: of pair s >> 1)
+        if constexpr (!FP4) {
+            // MXFP8, a pair of steps per iteration: the even step reads the
+            // pair's whole scale dwords (both 128-K halves; both halves of
+            // the pair were copied before step s - 1 ended), the odd step
+            // selects its bytes in the same registers (op_sel 2, 3), so
+            // scales are read once per pair instead of once per step.
+            uint32_t sy[2]; // A scales of M half 1
+            auto step = [&](int s, auto PC) {
+                constexpr int P = decltype(PC)::value;
+                const int r2 = r0 == 0 ? 2 : r0 - 1; // (r0 + 2) % 3
+                // X
+                issue_a(L, smem, 1, s + 1, wave);
+                if constexpr (P == 0) {
+                    read_sa<0, true>(rb, r0, 0u, sa);
+                    sb0 = read_sb<0, true>(rb, r0, 0u);
+                    sb1 = read_sb<1, true>(rb, r0, 0u);
+                }
+                read_a<0>(rb, P, fa);
+                read_b<0>(rb, P, fb0);
+                read_b<1>(rb, P, fb1);
+                part_sync<8 + kS>();
+                mma_two<FP4, F, 2 * P>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
+                part_sync<8 + kS>();
+                // Y
+                issue_a(L, smem, 0, s + 2, wave);
+                issue_b(L, smem, 0, s + 2, wave);
+                issue_b(L, smem, 1, s + 2, wave);
+                issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
+                if constexpr (P == 0)
+                    read_sa<1, true>(rb, r0, 0u, sy);
+                read_a<1>(rb, P, fa);
+                part_sync<8 + kS>();
+                mma_two<FP4, F, 2 * P>(acc[2], acc[3], fa, fb0, fb1, sy, sb0, sb1);
+                part_sync<8 + kS>();
+                if constexpr (P == 1)
+                    r0 = r0 == 2 ? 0 : r0 + 1;
+            };
+            for (int s = 0; s < nsteps; s += 2) {
+                step(s, std::integral_constant<int, 0>{});
+                if (s + 1 < nsteps)
+                    step(s + 1, std::integral_constant<int, 1>{});
+            }
+        } else
         for (int s = 0; s < nsteps; s++) {
             const int P = s & 1;
             const uint32_t hb = FP4 ? 0u : (uint32_t)P * 2;
