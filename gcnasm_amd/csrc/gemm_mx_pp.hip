@@ -428,15 +428,15 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
             }
         } else
         for (int s = 0; s < nsteps; s++) {
+            // MXFP4: one ring slot per step
             const int P = s & 1;
-            const uint32_t hb = FP4 ? 0u : (uint32_t)P * 2;
-            const int r1 = (FP4 || P) ? (r0 == 2 ? 0 : r0 + 1) : r0; // slot of step s + 1
-            const int r2 = r0 == 0 ? 2 : r0 - 1;                       // (r0 + 2) % 3
+            const int r1 = r0 == 2 ? 0 : r0 + 1; // slot of step s + 1
+            const int r2 = r0 == 0 ? 2 : r0 - 1; // (r0 + 2) % 3
             // X
             issue_a(L, smem, 1, s + 1, wave);
-            read_sa<0, FP4>(rb, r0, hb, sa);
-            sb0 = read_sb<0, FP4>(rb, r0, hb);
-            sb1 = read_sb<1, FP4>(rb, r0, hb);
+            read_sa<0, FP4>(rb, r0, 0u, sa);
+            sb0 = read_sb<0, FP4>(rb, r0, 0u);
+            sb1 = read_sb<1, FP4>(rb, r0, 0u);
             read_a<0>(rb, P, fa);
             read_b<0>(rb, P, fb0);
             read_b<1>(rb, P, fb1);
@@ -447,13 +447,9 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
             issue_a(L, smem, 0, s + 2, wave);
             issue_b(L, smem, 0, s + 2, wave);
             issue_b(L, smem, 1, s + 2, wave);
-            if constexpr (FP4) {
-                issue_s(L, smem, s + 2, 0, r2, wave);
-                issue_s(L, smem, s + 2, 1, r2, wave);
-            } else {
-                issue_s(L, smem, (s >> 1) + 2, P, r2, wave);
-            }
-            read_sa<1, FP4>(rb, r0, hb, sa);
+            issue_s(L, smem, s + 2, 0, r2, wave);
+            issue_s(L, smem, s + 2, 1, r2, wave);
+            read_sa<1, FP4>(rb, r0, 0u, sa);
             read_a<1>(rb, P, fa);
             part_sync<8 + kS>();
             mma_two<FP4, F>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
