@@ -822,8 +822,9 @@ def main():
         print(traffic_summary(args.traffic_summary, args.steps))
         return
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only (--gpus %d requested); the sharded "
-              "design is described in DESIGN.md" % args.gpus, file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (--gpus %d requested); a sharded run "
+              "(B split by columns, A replicated, no collective) is not built here"
+              % args.gpus, file=sys.stderr)
         sys.exit(2)
     legs = set(LEGS) if args.legs == "all" else set(args.legs.split(","))
     unknown = legs - set(LEGS)
