@@ -11,11 +11,14 @@
 //  * the A rows (<= 64, L2-resident) are loaded the same way, once per step
 //    for all NG groups, and multiply B with v_mfma_scale_f32_16x16x128_f8f6f4,
 //    one MFMA per 16 rows per group per step;
-//  * split-K: the gdz K slices of a column group run in waves of the same
-//    workgroup and are summed in LDS in slice order (slice 0 first), the
-//    order the split-K reduce uses, so no workspace is needed;
-//  * workgroup = T column tasks x KS slices (T * KS = 4 waves, or KS waves
-//    for KS = 8);
+//  * split-K: the gdz K slices of a column group are separate fp32 chains
+//    summed in slice order (slice 0 first), the order the split-K reduce
+//    uses, so no workspace is needed. For 1-16 rows one wave runs them in
+//    turn, so the split a caller asks for (which fixes the output bits) does
+//    not change the stream of loads; for more rows they run in waves of the
+//    same workgroup and are summed in LDS;
+//  * workgroup = T column tasks x KS slices (T * KS <= 8 waves; KS = 1 for
+//    1-16 rows);
 //  * MXFP4 (e2m1 packed two per byte): a step is 256 K = the same 128 bytes
 //    per row, so the loads are identical; two fp4 MFMAs per group and 16
 //    rows (K halves 0 and 1 of the step), one whole scale dword per step.
@@ -49,7 +52,7 @@ struct DecCfg {
     static constexpr int NG = NG_; // 16-column groups per wave
     static constexpr int D = XS > 0 ? XS
                            : DEEP ? (TM == 4 ? 4 : 6)
-                                  : TM == 1 ? (NG == 1 ? 8 : 6) : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
+                                  : TM == 1 ? 6 : (TM == 2 ? (NG == 1 ? 6 : 4) : (NG == 1 ? 4 : 3));
     static constexpr int MAX_WAVES = (DEEP || XS > 0) ? 4 : 8;
     // B scale dwords per step: a wave of the split variant with an even NG
     // starts at an even group, so groups 2j and 2j + 1 share the dword of one
@@ -120,16 +123,26 @@ __device__ __forceinline__ void dec_epilogue(const ga_f4gemm_kargs& args, const 
 }
 
 // F: the operands' 8-bit element formats (fmt_of_a / fmt_of_b; 0 for MXFP4).
-template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0, int F = 0>
+// LA (1-16 rows, in-workgroup): the workgroup's A panel, 16 rows x K, is
+// copied once into LDS (kLaBytes at most) and every wave reads its A
+// fragments from there instead of from L2 at every step.
+constexpr int kLaBytes = 128 * 1024;
+template <int TM, int NG_, bool BPS, bool FP4, bool DEEP, int XS = 0, int F = 0, bool LA = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(64, DecCfg<TM, NG_, DEEP, XS>::MAX_WAVES * 64)))
 void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__ ws,
                       const ga_splitk_ws_handle* __restrict__ wsh)
 {
     using Cfg = DecCfg<TM, NG_, DEEP, XS>;
+    static_assert(!LA || (TM == 1 && XS == 0), "LDS-resident A: 1-16 rows, in-workgroup");
     constexpr int kEPB = FP4 ? 2 : 1; // elements per byte
     constexpr int D = Cfg::D, NG = NG_, NB = Cfg::NB;
+    // 1-16 rows (in-workgroup variant): one wave runs all ks K slices of its
+    // column task, one fp32 chain each, the stream of loads unbroken across
+    // them; more rows: one wave per slice, summed through LDS
+    constexpr bool kSeq = XS == 0 && TM == 1;
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
-    constexpr int kLoadsPerStep = 2 * NG + 2 * TM + SA + NB;
+    constexpr int kLoadsA = LA ? 0 : 2 * TM; // A loads per step (LA: LDS reads)
+    constexpr int kLoadsPerStep = 2 * NG + kLoadsA + SA + NB;
     static_assert(kLoadsPerStep * (D - 1) < 64, "vmcnt range");
     // MXFP8 in-workgroup: a scale dword covers 256 K = two steps, so only the
     // even ring slots (the even steps: D is even) load scales and the odd
@@ -137,13 +150,18 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     // wait before slot J's MFMAs counts the D - 1 other slots' loads, issued
     // after slot J's: D/2 - 1 slots of J's parity and D/2 of the other.
     constexpr bool kPairScales = !FP4 && XS == 0 && D % 2 == 0;
-    constexpr int kLoadsOdd = kPairScales ? 2 * NG + 2 * TM : kLoadsPerStep;
+    constexpr int kLoadsOdd = kPairScales ? 2 * NG + kLoadsA : kLoadsPerStep;
     constexpr int kWaitEven =
         kPairScales ? (D / 2 - 1) * kLoadsPerStep + (D / 2) * kLoadsOdd : (D - 1) * kLoadsPerStep;
     constexpr int kWaitOdd =
         kPairScales ? (D / 2) * kLoadsPerStep + (D / 2 - 1) * kLoadsOdd : (D - 1) * kLoadsPerStep;
-    // in-workgroup K slices are summed through LDS (<= 8 waves)
-    __shared__ __attribute__((aligned(16))) float red[XS > 0 ? 4 : 8 * NG * TM * 256];
+    // loads of the D prologue steps, issued after the LA copies
+    constexpr int kWaitPro = kPairScales ? (D / 2) * (kLoadsPerStep + kLoadsOdd) : D * kLoadsPerStep;
+    static_assert(!LA || kWaitPro < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) char a_lds[LA ? kLaBytes : 16];
+    // in-workgroup K slices are summed through LDS (<= 8 waves; 1-16 rows sum
+    // them in registers)
+    __shared__ __attribute__((aligned(16))) float red[(XS > 0 || kSeq) ? 4 : 8 * NG * TM * 256];
     if constexpr (XS > 0) {
         if (gridDim.y > 1 && wsh && !(ws = resolve_ws(wsh, gridDim.y, args.M, args.N)))
             return; // workspace slot shorter than the split-K layout: write nothing
@@ -151,8 +169,9 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int slice = XS > 0 ? (int)blockIdx.y : wave % ks;
-    const int tl = XS > 0 ? wave : wave / ks;
+    const int kp = (XS > 0 || kSeq) ? 1 : ks; // waves per column task
+    const int slice = XS > 0 ? (int)blockIdx.y : wave % kp;
+    const int tl = XS > 0 ? wave : wave / kp;
     const int M = (int)args.M, N = (int)args.N, K = (int)args.K;
     // Workgroup b owns 16-column groups [b*G/nwg, (b+1)*G/nwg): equal shares
     // (within one group) for every CU; its waves take NG groups each. In the
@@ -172,8 +191,8 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     int kpt = K;
     if (XS > 0 ? gridDim.y > 1 : ks > 1)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
-    const int kb = slice * kpt;
-    const int ke = min(K, kb + kpt);
+    const int kb = kSeq ? 0 : slice * kpt;
+    const int ke = kSeq ? K : min(K, kb + kpt);
     const int nsteps = live ? max(0, (ke - kb) / (128 * kEPB)) : 0;
     const int kbb = kb / kEPB, Kb = K / kEPB; // bytes
 
@@ -184,13 +203,66 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         for (int i = 0; i < TM; i++)
             acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
 
+    // Sequential slices: each finished chain is added into tot, which starts
+    // at -0 (-0 + x == x for every x, signed zeros included), so tot is p0,
+    // p0 + p1, ... in slice order, the split-K reduce's order. A fold runs
+    // after a chain's last step: fold_at counts the wave's steps (never the
+    // final step, whose chain the fold after the loop takes).
+    v4f tot[kSeq ? NG : 1][kSeq ? TM : 1];
+    const int sps = kpt / (128 * kEPB); // steps per K slice
+    int fold_at = (kSeq && ks > 1 && sps < nsteps) ? sps : 0x7FFFFFFF;
+    auto fold = [&]() {
+        if constexpr (kSeq) {
+#pragma unroll
+            for (int c = 0; c < NG; c++) {
+                tot[c][0] = tot[c][0] + acc[c][0];
+                acc[c][0] = (v4f){0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    if constexpr (kSeq) {
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+            tot[c][0] = (v4f){-0.f, -0.f, -0.f, -0.f};
+    }
+    // after the MFMAs of step t (0-based within the wave's range)
+    auto fold_after = [&](int t) {
+        if constexpr (kSeq) {
+            if (t + 1 == fold_at) {
+                fold();
+                fold_at += sps;
+                if (fold_at >= nsteps)
+                    fold_at = 0x7FFFFFFF;
+            }
+        }
+    };
+
+    const int r = lane & 15, g = lane >> 4;
+    const uint32_t lda = args.stride_A0 / kEPB; // bytes
+    const long long abytes = (long long)M * lda;
+    const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
+    // A: lane 16g + r reads row 16i + r, K chunks g and g + 4 of the step
+    const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
+    if constexpr (LA) {
+        // Copy q = 2s + h of the panel: lane 16g + r copies row r, K chunk
+        // g + 4h of step s (rows past M read as zeros) to LDS byte
+        // q * 1024 + lane * 16, so lane 16g + r's operand of step s is at its
+        // own lane offset in copies 2s and 2s + 1. The waves take the copies
+        // in turn; a wave without columns waits for its own and meets the
+        // others at the barrier the working waves take after their prologue.
+        const int nw = (int)(blockDim.x >> 6);
+        const int ncopies = 2 * (K / (128 * kEPB));
+        for (int q = wave; q < ncopies; q += nw)
+            lds_load16(ra, (lds_void*)(a_lds + q * 1024),
+                       va + uni((uint32_t)(q >> 1) * 128 + (uint32_t)(q & 1) * 64), 0);
+        __builtin_amdgcn_sched_barrier(0); // the prologue's counted loads follow the copies
+        if (nsteps == 0) {
+            wait_vmcnt<0>();
+            barrier_lds();
+        }
+    }
+
     if (nsteps > 0) {
-        const int r = lane & 15, g = lane >> 4;
-        const uint32_t lda = args.stride_A0 / kEPB; // bytes
-        long long abytes = (long long)M * lda;
-        const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
-        // A: lane 16g + r reads row 16i + r, K chunks g and g + 4 of the step
-        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
         // B: groups past N read as zero (range-checked buffer)
         __amdgpu_buffer_rsrc_t rbuf;
         uint32_t vb, b_step, b_hi, b_grp;
@@ -241,12 +313,14 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                 v4i x1 = buf_load16_stream(rbuf, vb + uni(ob + c * b_grp + b_hi), 0);
                 fb[j][c] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
             }
+            if constexpr (!LA) {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const uint32_t oa = (uint32_t)s * 128 + (uint32_t)i * 16 * lda;
-                v4i y0 = buf_load16(ra, va + uni(oa), 0);
-                v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
-                fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+                for (int i = 0; i < TM; i++) {
+                    const uint32_t oa = (uint32_t)s * 128 + (uint32_t)i * 16 * lda;
+                    v4i y0 = buf_load16(ra, va + uni(oa), 0);
+                    v4i y1 = buf_load16(ra, va + uni(oa + 64), 0);
+                    fa[j][i] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+                }
             }
             if constexpr (!kPairScales || j % 2 == 0) {
                 const uint32_t q = (uint32_t)(FP4 ? s : (s >> 1)) * 256;
@@ -256,6 +330,15 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
 #pragma unroll
                 for (int c = 0; c < NB; c++)
                     fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
+            }
+        };
+        // LA: step s's A fragment from the panel in LDS
+        auto read_a = [&](int s, auto J) {
+            if constexpr (LA) {
+                constexpr int j = decltype(J)::value;
+                const v4i y0 = *(const v4i*)(a_lds + s * 2048 + lane * 16);
+                const v4i y1 = *(const v4i*)(a_lds + s * 2048 + 1024 + lane * 16);
+                fa[j][0] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
             }
         };
         // The odd step's scale operands, shifted out of the even slot's
@@ -372,6 +455,13 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
             load(min((int)J, nsteps - 1), J);
             __builtin_amdgcn_sched_barrier(0);
         });
+        if constexpr (LA) {
+            // the panel copies were issued before the prologue's loads: this
+            // wave's have landed, and after the barrier every wave's
+            wait_vmcnt<kWaitPro>();
+            barrier_lds();
+            static_for<D>([&](auto J) { read_a(min((int)J, nsteps - 1), J); });
+        }
         int s = 0;
         for (; s + D <= nsteps; s += D) {
             static_for<D>([&](auto J) {
@@ -381,13 +471,17 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                 } else {
                     mma(s + J, J);
                     load(min(s + D + (int)J, nsteps - 1), J);
+                    read_a(min(s + D + (int)J, nsteps - 1), J);
+                    fold_after(s + J);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
         static_for<D>([&](auto J) {
-            if ((int)J < nsteps - s)
+            if ((int)J < nsteps - s) {
                 mma(s + J, J);
+                fold_after(s + J);
+            }
         });
     }
 
@@ -399,7 +493,14 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         return;
     }
     // Sum the K slices of each column group in slice order, then the epilogue.
-    if (XS == 0 && ks > 1) {
+    if constexpr (kSeq) {
+        if (ks > 1) {
+            fold(); // the last slice
+#pragma unroll
+            for (int c = 0; c < NG; c++)
+                acc[c][0] = tot[c][0];
+        }
+    } else if (XS == 0 && ks > 1) {
         float* mine = red + ((tl * ks + slice) * NG * TM) * 256;
 #pragma unroll
         for (int c = 0; c < NG; c++)
@@ -681,18 +782,24 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
 }
 
 // Workgroups: one per CU (more when a CU's share needs over MAX_WAVES
-// waves), each with ceil(share / NG) column tasks x ks slices (ks <= MAX_WAVES).
-template <int TM, int NG, bool BPS, bool FP4, bool DEEP = false, int F = 0>
+// waves), each with ceil(share / NG) column tasks x kp waves per task: one
+// (all ks K slices in turn) for 1-16 rows, else one per slice (ks <=
+// MAX_WAVES). Measured on MI355X (1-16 rows, three rotated weight sets, each
+// split timed after a discarded first run of the shape): one wave per task is
+// as fast as the fastest split -- N = 8192, K = 28672, 16 rows: 37.1 us at
+// one slice, 37.1-38.3 with one wave per slice at 2-8 slices.
+template <int TM, int NG, bool BPS, bool FP4, bool DEEP = false, int F = 0, bool LA = false>
 void launch_dec(const ga_f4gemm_kargs& args, int ks, int num_cu, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
-    const int max_tasks = DecCfg<TM, NG, DEEP>::MAX_WAVES / ks; // waves per workgroup
+    const int kp = TM == 1 ? 1 : ks;
+    const int max_tasks = DecCfg<TM, NG, DEEP>::MAX_WAVES / kp; // tasks per workgroup
     int nwg = std::min(num_cu, (groups + NG - 1) / NG);
     nwg = std::max(nwg, (groups + NG * max_tasks - 1) / (NG * max_tasks));
     const int share = (groups + nwg - 1) / nwg;
     const int tasks = (share + NG - 1) / NG;
-    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP, 0, F>), dim3(nwg),
-                       dim3(64 * tasks * ks), 0, stream, args, nwg, ks, nullptr, nullptr);
+    hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, DEEP, 0, F, LA>), dim3(nwg),
+                       dim3(64 * tasks * kp), 0, stream, args, nwg, ks, nullptr, nullptr);
 }
 
 // Split variant: one wave of NG groups per workgroup per K slice, grid
@@ -750,11 +857,31 @@ void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int nwg, float* ws,
                            args, nwg, ws, wsh);
 }
 
+bool la_fits(const ga_f4gemm_kargs& args, bool fp4, int num_cu)
+{
+    const long long steps = (long long)args.K / (fp4 ? 256 : 128);
+    const int groups = (int)args.N / 16;
+    const int nwg = std::max(1, std::min(num_cu, groups));
+    return steps * 2048 <= kLaBytes && (groups + nwg - 1) / nwg >= 4;
+}
+
 template <bool BPS, bool FP4, int F>
 void launch_dec_rows(const ga_f4gemm_kargs& args, int gdz, int num_cu, hipStream_t stream)
 {
     const int tm = ((int)args.M + 15) / 16;
-    if (tm == 1)
+    // 1-16 rows: A rows past M read as zeros without memory traffic, so up to
+    // 8 rows a wave per 16-column group (more waves, A bytes still small)
+    // streams fastest; 9-16 rows two groups per wave, which halves A's bytes
+    // (measured on MI355X, N = 28672, K = 8192: 1-4 rows 36.9-37.1 us
+    // against 39.1-39.4; 8 rows 37.7 against 39.5; 16 rows 43.0 against 40.1)
+    // 9-16 rows with the A panel (16 x K bytes) within kLaBytes and at least
+    // four groups per CU (waves to share its copies): a wave per group too,
+    // A read from LDS (la_fits)
+    if (tm == 1 && args.M <= 8)
+        launch_dec<1, 1, BPS, FP4, false, F>(args, gdz, num_cu, stream);
+    else if (tm == 1 && la_fits(args, FP4, num_cu))
+        launch_dec<1, 1, BPS, FP4, false, F, true>(args, gdz, num_cu, stream);
+    else if (tm == 1)
         launch_dec<1, 2, BPS, FP4, false, F>(args, gdz, num_cu, stream);
     else if (tm == 2) {
         // 17-32 rows: six steps in flight for one two-group task per CU and

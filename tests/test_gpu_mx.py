@@ -231,6 +231,43 @@ def test_decode_path(dev, M, NKL):
           (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
+# 1-16 rows with a split: one wave runs all K slices of its column task in
+# turn, one fp32 chain per slice, the slices summed in order. Every N has
+# one group per wave at 1 row and two at 16 (N = 16384 / 28672: 4-7 groups
+# per workgroup; N = 784 and 4096: 1-2); K = 1152 at l2 = 2 is 3 slices
+# (512, 512, 128), the last one step.
+@pytest.mark.parametrize("M", [1, 12, 16])
+@pytest.mark.parametrize("NKL", [(16384, 2048, 1), (16384, 2048, 3), (16384, 1152, 2),
+                                 (28672, 1024, 2), (784, 1152, 2), (4096, 3072, 3),
+                                 (4096, 1152, 2)])
+def test_decode_sequential_slices(dev, M, NKL):
+    N, K, l2 = NKL
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_128x512_splitK")
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=300 + M + l2, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    check(got, expect(qa, sa, qb, sb, l2), "decode sequential slices M=%d N=%d K=%d gdz=%d" %
+          (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
+# 9-16 rows with at least four 16-column groups per CU and K <= 8192: the
+# workgroup's A panel (16 rows x K) is copied into LDS once and the waves read
+# their A fragments there. K = 8192 fills the 128 KB panel; K = 1152 is 9
+# steps; N = 20480 gives five groups per CU; N = 16384 + 64 gives 4 or 5
+# groups per CU on five waves, so most workgroups hold a wave without columns
+# (it takes its share of the copies and the barrier); M = 9 leaves 7 rows of
+# the panel zero.
+@pytest.mark.parametrize("M", [9, 12, 16])
+@pytest.mark.parametrize("NKL", [(16384, 8192, 0), (20480, 1152, 0), (20480, 1152, 1),
+                                 (16384 + 64, 2048, 2), (28672, 8192, 3)])
+def test_decode_a_panel_in_lds(dev, M, NKL):
+    N, K, l2 = NKL
+    cfg = cfg_named("ga_mxfp8_bf16_BpreShuffle_128x512" + ("_splitK" if l2 else ""))
+    qa, sa, qb, sb = mx_operands(M, N, K, seed=400 + M + l2, std_b=0.02)
+    got, ld = run_mx(dev, qa, sa, qb, sb, cfg, l2)
+    check(got, expect(qa, sa, qb, sb, l2), "decode A panel in LDS M=%d N=%d K=%d gdz=%d" %
+          (M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
+
+
 @pytest.mark.parametrize("MNK", [(40, 8192, 8192), (64, 8192, 8192), (64, 16384, 1024),
                                  (48, 4096, 2048), (24, 8192, 8192)])
 def test_decode_64_rows_paths(dev, MNK):

@@ -179,6 +179,20 @@ def test_fp4_decode_path(dev, M, NKL):
     check4(got, qa, sa, qb, sb, l2, "decode M=%d N=%d K=%d L=%d" % (M, N, K, l2))
 
 
+@pytest.mark.parametrize("M", [1, 12, 16])
+@pytest.mark.parametrize("NKL", [(16384, 2048, 1), (16384, 2304, 2), (4096, 4096, 3),
+                                 (784, 1280, 2), (16384, 16384, 0), (28672, 8192, 1)])
+def test_fp4_decode_sequential_slices(dev, M, NKL):
+    """1-16 rows, MXFP4: several K slices per wave (one fp32 chain each,
+    summed in slice order), as for MXFP8; at 12 and 16 rows with wide N the
+    A panel in LDS (K = 16384 fills its 128 KB)."""
+    N, K, l2 = NKL
+    qa, sa, qb, sb = mx4_operands(M, N, K, seed=M * 17 + l2)
+    got = run_mx4(dev, qa, sa, qb, sb, cfg4("ga_mxfp4_bf16_BpreShuffle_256x256_splitK"), l2)
+    check4(got, qa, sa, qb, sb, l2, "decode sequential slices M=%d N=%d K=%d L=%d" %
+           (M, N, K, l2))
+
+
 def test_fp4_decode_deep(dev):
     """33-64 rows, one two-group task per CU and long K: the decode kernel
     with four steps in flight."""
