@@ -51,17 +51,19 @@ void launch_mx4_pp_nobps(const ga_f4gemm_kargs& args, float* ws, const ga_splitk
 bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz);
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int fmt,
                       int num_cu, hipStream_t stream);
-// 17-64 rows, each wave over ng (2-8) 16-column groups and one K slice, the
-// slices in separate workgroups (gemm_mx_decode.hip): mx_decode_split_groups
-// gives ng for the shape (0: not this path); with gdz > 1 the slices write
-// fp32 partials to the split-K workspace (ws, or the slot wsh) for the
-// split-K reduce, with gdz = 1 the kernel applies the epilogue (33-64 rows:
-// in the shared-A variant, four waves per workgroup sharing A through LDS,
-// sized from num_cu).
-int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu);
-void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, int num_cu,
-                            hipStream_t stream);
+// 17-64 rows, each wave over ng (2-8) 16-column groups, the caller's gdz K
+// slices on phys workgroups along K, each running ceil(gdz / phys)
+// consecutive slices as separate fp32 chains (gemm_mx_decode.hip):
+// mx_decode_split_groups gives ng and phys for the shape (ng 0: not this
+// path). With phys > 1 each slice's fp32 partials go to the split-K
+// workspace (ws, or the slot wsh) for the split-K reduce; with phys = 1 the
+// kernel sums the slices in order and applies the epilogue, no workspace
+// (33-64 rows: in the shared-A variant, four waves per workgroup sharing A
+// through LDS, sized from num_cu).
+int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu, int* phys);
+void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, bool bps,
+                            bool fp4, int fmt, float* ws, const ga_splitk_ws_handle* wsh,
+                            int num_cu, hipStream_t stream);
 // fmt (the decode entry points and launch_mx_pp_fmt): MXFP8 operand element
 // formats, fmt(A) | fmt(B) << 1 with 0 E4M3, 1 E5M2; 0 for MXFP4.
 // 256x256 eight-wave kernel with operand formats fmt, grid of its own tiles.

@@ -1004,10 +1004,18 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
         if (st != GA_OK)
             return st;
     }
-    const int split_groups = decode ? mx_decode_split_groups(*args, gdz, num_cu) : 0;
+    int phys = gdz; // workgroups along K of the 17-64-row decode kernels
+    const int split_groups = decode ? mx_decode_split_groups(*args, gdz, num_cu, &phys) : 0;
     if (decode && split_groups == 0) {
         // few rows: stream B, K slices summed inside the kernel (no workspace)
         launch_mx_decode(*args, gdz, k.cfg.bpreshuffle != 0, k.elem_bits == 4, fmt, num_cu, s);
+        GA_HIP_CHECK(hipGetLastError());
+        return GA_OK;
+    }
+    if (decode && phys == 1) {
+        // 17-64 rows, every K slice in one workgroup along K (no workspace)
+        launch_mx_decode_split(*args, gdz, 1, split_groups, k.cfg.bpreshuffle != 0,
+                               k.elem_bits == 4, fmt, nullptr, nullptr, num_cu, s);
         GA_HIP_CHECK(hipGetLastError());
         return GA_OK;
     }
@@ -1043,7 +1051,7 @@ static ga_status kernel_launch(int idx, const ga_f4gemm_kargs* args, int gdx, in
         }
     }
     if (split_groups > 0)
-        launch_mx_decode_split(*args, gdz, split_groups, k.cfg.bpreshuffle != 0, k.elem_bits == 4,
+        launch_mx_decode_split(*args, gdz, phys, split_groups, k.cfg.bpreshuffle != 0, k.elem_bits == 4,
                                fmt, ws, wsh, num_cu, s);
     else if (fmt != 0)
         launch_mx_pp_fmt(*args, ws, gdz > 1 ? wsh : nullptr, gdz, k.cfg.bpreshuffle != 0, fmt, s);

@@ -138,8 +138,12 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     constexpr int D = Cfg::D, NG = NG_, NB = Cfg::NB;
     // 1-16 rows (in-workgroup variant): one wave runs all ks K slices of its
     // column task, one fp32 chain each, the stream of loads unbroken across
-    // them; more rows: one wave per slice, summed through LDS
+    // them; more rows: one wave per slice, summed through LDS. Split variant:
+    // the ks K slices run on gridDim.y workgroups along K, each taking
+    // kseq = ceil(ks / gridDim.y) <= 2 consecutive slices (all of them when
+    // gridDim.y is 1, for up to 32 rows).
     constexpr bool kSeq = XS == 0 && TM == 1;
+    constexpr bool kFoldTot = kSeq || (XS > 0 && TM <= 2); // chains summed in registers
     constexpr int SA = (TM + 1) / 2; // A scale dwords (32-row blocks)
     constexpr int kLoadsA = LA ? 0 : 2 * TM; // A loads per step (LA: LDS reads)
     constexpr int kLoadsPerStep = 2 * NG + kLoadsA + SA + NB;
@@ -160,10 +164,12 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     static_assert(!LA || kWaitPro < 64, "vmcnt range");
     __shared__ __attribute__((aligned(16))) char a_lds[LA ? kLaBytes : 16];
     // in-workgroup K slices are summed through LDS (<= 8 waves; 1-16 rows sum
-    // them in registers)
+    // them in registers); the split variant parks the first of its two
+    // chains in LDS until both are stored
     __shared__ __attribute__((aligned(16))) float red[(XS > 0 || kSeq) ? 4 : 8 * NG * TM * 256];
+    __shared__ __attribute__((aligned(16))) float park[XS > 0 ? NG * TM * 256 : 4];
     if constexpr (XS > 0) {
-        if (gridDim.y > 1 && wsh && !(ws = resolve_ws(wsh, gridDim.y, args.M, args.N)))
+        if (gridDim.y > 1 && wsh && !(ws = resolve_ws(wsh, ks, args.M, args.N)))
             return; // workspace slot shorter than the split-K layout: write nothing
     }
 
@@ -189,10 +195,13 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     const bool live = ng_here > 0;
 
     int kpt = K;
-    if (XS > 0 ? gridDim.y > 1 : ks > 1)
+    if (ks > 1)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
-    const int kb = kSeq ? 0 : slice * kpt;
-    const int ke = kSeq ? K : min(K, kb + kpt);
+    // the wave's K slices: [z0, z0 + kseq) (kSeq: all of them)
+    const int kseq = kSeq ? ks : XS > 0 ? (ks + (int)gridDim.y - 1) / (int)gridDim.y : 1;
+    const int z0 = kSeq ? 0 : slice * kseq;
+    const int kb = z0 * kpt;
+    const int ke = min(K, kb + kseq * kpt);
     const int nsteps = live ? max(0, (ke - kb) / (128 * kEPB)) : 0;
     const int kbb = kb / kEPB, Kb = K / kEPB; // bytes
 
@@ -208,26 +217,47 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     // p0 + p1, ... in slice order, the split-K reduce's order. A fold runs
     // after a chain's last step: fold_at counts the wave's steps (never the
     // final step, whose chain the fold after the loop takes).
-    v4f tot[kSeq ? NG : 1][kSeq ? TM : 1];
+    // Split variant over several workgroups: the wave's first chain is
+    // parked in LDS at the fold (a store there would count in vmcnt beside
+    // the stream's counted loads), both are stored at the end.
+    v4f tot[kFoldTot ? NG : 1][kFoldTot ? TM : 1];
     const int sps = kpt / (128 * kEPB); // steps per K slice
-    int fold_at = (kSeq && ks > 1 && sps < nsteps) ? sps : 0x7FFFFFFF;
+    const bool in_regs = XS == 0 || gridDim.y == 1; // chains summed in tot
+    int fold_at = ((kSeq || XS > 0) && kseq > 1 && sps < nsteps) ? sps : 0x7FFFFFFF;
     auto fold = [&]() {
-        if constexpr (kSeq) {
+        if constexpr (kFoldTot) {
+            if (in_regs) {
 #pragma unroll
-            for (int c = 0; c < NG; c++) {
-                tot[c][0] = tot[c][0] + acc[c][0];
-                acc[c][0] = (v4f){0.f, 0.f, 0.f, 0.f};
+                for (int c = 0; c < NG; c++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        tot[c][i] = tot[c][i] + acc[c][i];
+                        acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+                    }
+            }
+        }
+        if constexpr (XS > 0) {
+            if (!in_regs) {
+#pragma unroll
+                for (int c = 0; c < NG; c++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        *(v4f*)(park + (c * TM + i) * 256 + lane * 4) = acc[c][i];
+                        acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+                    }
             }
         }
     };
-    if constexpr (kSeq) {
+    if constexpr (kFoldTot) {
 #pragma unroll
         for (int c = 0; c < NG; c++)
-            tot[c][0] = (v4f){-0.f, -0.f, -0.f, -0.f};
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                tot[c][i] = (v4f){-0.f, -0.f, -0.f, -0.f};
     }
     // after the MFMAs of step t (0-based within the wave's range)
     auto fold_after = [&](int t) {
-        if constexpr (kSeq) {
+        if constexpr (kSeq || XS > 0) {
             if (t + 1 == fold_at) {
                 fold();
                 fold_at += sps;
@@ -468,6 +498,7 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                 wait_vmcnt<(decltype(J)::value % 2 == 0) ? kWaitEven : kWaitOdd>();
                 if constexpr (XS > 0) {
                     mma_load(s + J, min(s + D + (int)J, nsteps - 1), J);
+                    fold_after(s + J);
                 } else {
                     mma(s + J, J);
                     load(min(s + D + (int)J, nsteps - 1), J);
@@ -485,20 +516,36 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         });
     }
 
-    // Split variant: this slice's fp32 partials to the workspace; one slice:
-    // the epilogue below.
-    if (XS > 0 && gridDim.y > 1) {
-        if (live)
-            dec_store_partials<NG, TM>(ws, acc, slice, cg0, ng_here, M, N, lane);
-        return;
+    // Split variant: this workgroup's K slices' fp32 partials to the
+    // workspace (the parked first chain, then the last); one workgroup along
+    // K: the epilogue below.
+    if constexpr (XS > 0) {
+        if (gridDim.y > 1) {
+            if (live) {
+                int z = z0;
+                if (kseq > 1 && ke - kb > kpt) {
+                    v4f first[NG][TM];
+#pragma unroll
+                    for (int c = 0; c < NG; c++)
+#pragma unroll
+                        for (int i = 0; i < TM; i++)
+                            first[c][i] = *(const v4f*)(park + (c * TM + i) * 256 + lane * 4);
+                    dec_store_partials<NG, TM>(ws, first, z++, cg0, ng_here, M, N, lane);
+                }
+                dec_store_partials<NG, TM>(ws, acc, z, cg0, ng_here, M, N, lane);
+            }
+            return;
+        }
     }
     // Sum the K slices of each column group in slice order, then the epilogue.
-    if constexpr (kSeq) {
+    if constexpr (kFoldTot) {
         if (ks > 1) {
             fold(); // the last slice
 #pragma unroll
             for (int c = 0; c < NG; c++)
-                acc[c][0] = tot[c][0];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    acc[c][i] = tot[c][i];
         }
     } else if (XS == 0 && ks > 1) {
         float* mine = red + ((tl * ks + slice) * NG * TM) * 256;
@@ -575,8 +622,12 @@ struct LaCfg {
     static_assert(kWaitOdd < 64 && kWaitEven < 64, "vmcnt range");
 };
 
+// ks: the caller's K slices; with gridDim.y == 1 the waves run them in turn
+// (one fp32 chain each, summed in slice order in registers) and apply the
+// epilogue, else gridDim.y == ks and each workgroup writes its slice's
+// partials.
 template <int TM, int NG, bool BPS, bool FP4, int F>
-__global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args, int nwg,
+__global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args, int nwg, int ks,
                                                            float* __restrict__ ws,
                                                            const ga_splitk_ws_handle* __restrict__ wsh)
 {
@@ -599,21 +650,44 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
     const bool live = ng_here > 0;
 
     int kpt = K;
-    if (gridDim.y > 1)
+    if (ks > 1)
         kpt = ((K >> args.log2_k_split) + 255) / 256 * 256;
-    const int kb = slice * kpt;
-    const int ke = min(K, kb + kpt);
+    const bool seq = gridDim.y == 1; // every slice in this workgroup
+    const int kb = seq ? 0 : slice * kpt;
+    const int ke = seq ? K : min(K, kb + kpt);
     // the same for every wave of the workgroup: all of them copy A and meet
     // at every step's barrier, with or without columns of their own
     const int nsteps = max(0, (ke - kb) / (128 * kEPB));
     const int kbb = kb / kEPB, Kb = K / kEPB; // bytes
 
-    v4f acc[NG][TM];
+    v4f acc[NG][TM], tot[NG][TM];
 #pragma unroll
     for (int c = 0; c < NG; c++)
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++) {
             acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+            tot[c][i] = (v4f){-0.f, -0.f, -0.f, -0.f}; // -0 + x == x
+        }
+    // slices in turn: each finished chain is added into tot, in slice order
+    const int sps = kpt / (128 * kEPB);
+    int fold_at = (seq && ks > 1 && sps < nsteps) ? sps : 0x7FFFFFFF;
+    auto fold = [&]() {
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                tot[c][i] = tot[c][i] + acc[c][i];
+                acc[c][i] = (v4f){0.f, 0.f, 0.f, 0.f};
+            }
+    };
+    auto fold_after = [&](int t) {
+        if (t + 1 == fold_at) {
+            fold();
+            fold_at += sps;
+            if (fold_at >= nsteps)
+                fold_at = 0x7FFFFFFF;
+        }
+    };
 
     if (nsteps > 0) {
         const int r = lane & 15, g = lane >> 4;
@@ -759,6 +833,7 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
                 __builtin_amdgcn_sched_barrier(0);
                 mma(s + j, J);
                 load_bs(min(s + j + D, nsteps - 1), J);
+                fold_after(s + j);
                 __builtin_amdgcn_sched_barrier(0);
             });
         }
@@ -768,6 +843,7 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
             if ((int)J < nsteps - s) {
                 read_a(J);
                 mma(s + J, J);
+                fold_after(s + J);
             }
         });
     }
@@ -776,6 +852,14 @@ __global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args,
         if (live)
             dec_store_partials<NG, TM>(ws, acc, slice, cg0, ng_here, M, N, lane);
         return;
+    }
+    if (ks > 1) {
+        fold(); // the last slice
+#pragma unroll
+        for (int c = 0; c < NG; c++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                acc[c][i] = tot[c][i];
     }
     if (live)
         dec_epilogue<NG, TM>(args, acc, cg0, ng_here, lane);
@@ -815,46 +899,47 @@ constexpr int xs_depth()
 }
 
 template <int TM, int NG, bool BPS, bool FP4, int F>
-void launch_dec_xs(const ga_f4gemm_kargs& args, int gdz, float* ws, const ga_splitk_ws_handle* wsh,
-                   hipStream_t stream)
+void launch_dec_xs(const ga_f4gemm_kargs& args, int gdz, int phys, float* ws,
+                   const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
     const int tasks = (groups + NG - 1) / NG;
     hipLaunchKernelGGL((mx_decode_kernel<TM, NG, BPS, FP4, false, xs_depth<TM, NG, FP4>(), F>),
-                       dim3(tasks, gdz), dim3(64), 0, stream, args, tasks, 1, ws, wsh);
+                       dim3(tasks, phys), dim3(64), 0, stream, args, tasks, gdz, ws, wsh);
 }
 
 template <int TM, bool BPS, bool FP4, int F>
-void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
+void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, float* ws,
                       const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
     if (!BPS || F != 0) // row-major B, and E5M2 operands: the two extremes only
         ng = ng <= 2 ? 2 : 8;
     switch (ng) {
-    case 2: launch_dec_xs<TM, 2, BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
-    case 4: launch_dec_xs<TM, (F ? 8 : 4), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
-    case 5: launch_dec_xs<TM, (F ? 8 : 5), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
-    case 6: launch_dec_xs<TM, (F ? 8 : 6), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
-    case 7: launch_dec_xs<TM, (F ? 8 : 7), BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
-    default: launch_dec_xs<TM, 8, BPS, FP4, F>(args, gdz, ws, wsh, stream); break;
+    case 2: launch_dec_xs<TM, 2, BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
+    case 4: launch_dec_xs<TM, (F ? 8 : 4), BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
+    case 5: launch_dec_xs<TM, (F ? 8 : 5), BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
+    case 6: launch_dec_xs<TM, (F ? 8 : 6), BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
+    case 7: launch_dec_xs<TM, (F ? 8 : 7), BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
+    default: launch_dec_xs<TM, 8, BPS, FP4, F>(args, gdz, phys, ws, wsh, stream); break;
     }
 }
 
-// Shared-A split variant: nwg workgroups per slice, each wave up to 2 (a
+// Shared-A split variant: nwg workgroups per slice (phys == gdz), or all
+// gdz slices in turn in each workgroup (phys == 1); each wave up to 2 (a
 // share of at most 8 groups) or 4 of its workgroup's groups.
 template <bool BPS, bool FP4, int F>
-void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int nwg, float* ws,
+void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int phys, int nwg, float* ws,
                    const ga_splitk_ws_handle* wsh, hipStream_t stream)
 {
     const int groups = (int)args.N / 16;
     const int share = (groups + nwg - 1) / nwg;
-    const dim3 grid(nwg, gdz);
+    const dim3 grid(nwg, phys);
     if (share <= 8)
         hipLaunchKernelGGL((mx_decode_la_kernel<4, 2, BPS, FP4, F>), grid, dim3(256), 0, stream,
-                           args, nwg, ws, wsh);
+                           args, nwg, gdz, ws, wsh);
     else
         hipLaunchKernelGGL((mx_decode_la_kernel<4, 4, BPS, FP4, F>), grid, dim3(256), 0, stream,
-                           args, nwg, ws, wsh);
+                           args, nwg, gdz, ws, wsh);
 }
 
 bool la_fits(const ga_f4gemm_kargs& args, bool fp4, int num_cu)
@@ -918,21 +1003,37 @@ bool mx_decode_applies(const ga_f4gemm_kargs& args, int gdz)
     return args.M >= 1 && args.M <= 64 && gdz <= 8;
 }
 
-int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
+int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu, int* phys)
 {
+    *phys = gdz;
     if (args.M <= 16 || args.M > 64 || gdz > 8 || num_cu <= 0)
         return 0;
-    // waves (tasks x slices) in whole rounds of one per CU, as few rounds as
-    // eight groups per wave allow, the groups spread evenly over them
-    // (N = 28672, one slice: 7 groups, 256 waves; N = 8192, 4 slices: 8)
-    const long long work = (long long)(args.N / 16) * gdz;
+    // Workgroups along K (phys) for the caller's gdz K slices, each running
+    // consecutive slices as separate fp32 chains (so the output bits are the
+    // split's whatever phys is): one when that gives a wave five or more
+    // 16-column groups, else enough for eight groups per wave, with at most
+    // two slices per workgroup. Measured on MI355X at 64 rows (best of 100
+    // calls, one workgroup per slice): N = 28672, K = 8192: 45.0 us with one
+    // workgroup along K (shared-A variant), 48.6 us with two; N = 8192,
+    // K = 28672: 46.3 us at four (8 groups per wave), 50.2 at two, 50.9 at
+    // eight.
+    const long long groups = args.N / 16;
+    int p = 1;
+    if (groups < 5LL * num_cu)
+        p = std::min(gdz, std::max((gdz + 1) / 2, (int)((8LL * num_cu + groups - 1) / groups)));
+    // waves (tasks x workgroups along K) in whole rounds of one per CU, as
+    // few rounds as eight groups per wave allow, the groups spread evenly
+    // over them (N = 28672, one along K: 7 groups, 256 waves; N = 8192, four:
+    // 8)
+    const long long work = groups * p;
     const long long rounds = (work + 8LL * num_cu - 1) / (8LL * num_cu);
     int ng = (int)((work + rounds * num_cu - 1) / (rounds * num_cu));
     ng = ng < 2 ? 2 : (ng == 3 ? 4 : ng);
-    // one slice: only when a wave gets at least five groups (narrower N
-    // keeps the in-workgroup kernel, which needs no partials either way)
-    if (gdz == 1 && ng < 5)
+    // one slice at fewer than five groups per wave: the in-workgroup kernel
+    // (it needs no partials either)
+    if (p == 1 && ng < 5)
         return 0;
+    *phys = p;
     return ng;
 }
 
@@ -954,59 +1055,64 @@ int la_workgroups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
 // variant stays (M = 64, N = 8192, K = 28672 at 4 slices: 47.6 us, shared-A
 // 51.0: the fp32 partials and the reduce cost the same, the shared-A kernel
 // streams ~7 % slower there).
+// phys == 1 at 33-64 rows: the shared-A variant. The split variant with
+// phys == 1 runs at most 32 rows (its 64-row waves have no registers for the
+// running sum of the slices).
 template <bool BPS, bool FP4, int F>
-void launch_split_t(const ga_f4gemm_kargs& args, int gdz, int ng, float* ws,
+void launch_split_t(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, float* ws,
                     const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
 {
-    if (args.M > 32 && gdz == 1 && num_cu > 0)
-        launch_dec_la<BPS, FP4, F>(args, 1, la_workgroups(args, 1, num_cu), ws, wsh, stream);
+    if (args.M > 32 && phys == 1 && num_cu > 0)
+        launch_dec_la<BPS, FP4, F>(args, gdz, 1, la_workgroups(args, 1, num_cu), ws, wsh, stream);
     else if (args.M > 32)
-        launch_dec_xs_ng<4, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
+        launch_dec_xs_ng<4, BPS, FP4, F>(args, gdz, phys, ng, ws, wsh, stream);
     else
-        launch_dec_xs_ng<2, BPS, FP4, F>(args, gdz, ng, ws, wsh, stream);
+        launch_dec_xs_ng<2, BPS, FP4, F>(args, gdz, phys, ng, ws, wsh, stream);
 }
 
 template <bool FP4, int F>
-void launch_both(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, float* ws,
+void launch_both(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, bool bps, float* ws,
                  const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
 {
     if (ng > 0)
-        bps ? launch_split_t<true, FP4, F>(args, gdz, ng, ws, wsh, num_cu, stream)
-            : launch_split_t<false, FP4, F>(args, gdz, ng, ws, wsh, num_cu, stream);
+        bps ? launch_split_t<true, FP4, F>(args, gdz, phys, ng, ws, wsh, num_cu, stream)
+            : launch_split_t<false, FP4, F>(args, gdz, phys, ng, ws, wsh, num_cu, stream);
     else
         bps ? launch_dec_rows<true, FP4, F>(args, gdz, num_cu, stream)
             : launch_dec_rows<false, FP4, F>(args, gdz, num_cu, stream);
 }
 
-// ng > 0: the split variant (ws / wsh), else the in-workgroup kernel.
-void launch_any(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4, int fmt,
-                float* ws, const ga_splitk_ws_handle* wsh, int num_cu, hipStream_t stream)
+// ng > 0: the split variant (ws / wsh when phys > 1), else the in-workgroup
+// kernel.
+void launch_any(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, bool bps, bool fp4,
+                int fmt, float* ws, const ga_splitk_ws_handle* wsh, int num_cu,
+                hipStream_t stream)
 {
     if (fp4) {
-        launch_both<true, 0>(args, gdz, ng, bps, ws, wsh, num_cu, stream);
+        launch_both<true, 0>(args, gdz, phys, ng, bps, ws, wsh, num_cu, stream);
         return;
     }
     switch (fmt) {
-    case 1: launch_both<false, 1>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
-    case 2: launch_both<false, 2>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
-    case 3: launch_both<false, 3>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
-    default: launch_both<false, 0>(args, gdz, ng, bps, ws, wsh, num_cu, stream); break;
+    case 1: launch_both<false, 1>(args, gdz, phys, ng, bps, ws, wsh, num_cu, stream); break;
+    case 2: launch_both<false, 2>(args, gdz, phys, ng, bps, ws, wsh, num_cu, stream); break;
+    case 3: launch_both<false, 3>(args, gdz, phys, ng, bps, ws, wsh, num_cu, stream); break;
+    default: launch_both<false, 0>(args, gdz, phys, ng, bps, ws, wsh, num_cu, stream); break;
     }
 }
 
 } // namespace
 
-void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int ng, bool bps, bool fp4,
-                            int fmt, float* ws, const ga_splitk_ws_handle* wsh, int num_cu,
-                            hipStream_t stream)
+void launch_mx_decode_split(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, bool bps,
+                            bool fp4, int fmt, float* ws, const ga_splitk_ws_handle* wsh,
+                            int num_cu, hipStream_t stream)
 {
-    launch_any(args, gdz, ng, bps, fp4, fmt, ws, wsh, num_cu, stream);
+    launch_any(args, gdz, phys, ng, bps, fp4, fmt, ws, wsh, num_cu, stream);
 }
 
 void launch_mx_decode(const ga_f4gemm_kargs& args, int gdz, bool bps, bool fp4, int fmt,
                       int num_cu, hipStream_t stream)
 {
-    launch_any(args, gdz, 0, bps, fp4, fmt, nullptr, nullptr, num_cu, stream);
+    launch_any(args, gdz, gdz, 0, bps, fp4, fmt, nullptr, nullptr, num_cu, stream);
 }
 
 } // namespace ga
