@@ -270,9 +270,11 @@ def quant_legs(torch, steps, warmup):
         for name, fn, nbytes in legs:
             us = time_call(torch, lambda: _lib.check(fn()), steps, warmup)
             gbs = nbytes / (us * 1e-6) / 1e9
-            out.append({"workload": "quant_%s_%dx%d_%s" % (name, n, n, "f32" if eb == 4 else "bf16"),
+            wl = "quant_%s_%dx%d_%s" % (name, n, n, "f32" if eb == 4 else "bf16")
+            out.append({"workload": wl,
                         "value": round(gbs, 1), "unit": "GB/s", "kernel_avg_us": round(us, 2),
-                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(nbytes)})
+                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(nbytes),
+                        "roofline": roofline(wl, gbs, "hbm", HBM_PEAK_GBS, "GB/s")})
         del x
     del q8, q4, s32, sfa, sfb
     torch.cuda.empty_cache()
@@ -331,9 +333,11 @@ def mxfp4_leg(torch, ops, f4gemm, steps, warmup):
                       "tflops": round(fl / rr["avg_us"] / 1e6, 1),
                       "reference_us": ref_us,
                       "vs_reference": round(ref_us / rr["avg_us"], 4)})
-    return {"workload": "mxfp4_gemm_8192x8192x8192", "value": round(tf, 1), "unit": "TFLOP/s",
+    wl = "mxfp4_gemm_8192x8192x8192"
+    return {"workload": wl, "value": round(tf, 1), "unit": "TFLOP/s",
             "kernel": r["cfg"].knl_name, "kernel_avg_us": round(r["avg_us"], 2),
             "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+            "roofline": roofline(wl, tf, "mfma", FP4_PEAK_TFLOPS, "TFLOP/s", r["cfg"].knl_name),
             "data": "quantised N(0,1)*2^U[-4,4]",
             "reference_published": REF_MXFP4_8192_TFLOPS,
             "vs_reference": table[0]["vs_reference"],
@@ -352,10 +356,13 @@ def mxfp4_decode_leg(torch, ops, f4gemm, steps, warmup):
     torch.cuda.empty_cache()
     dbytes = dM * dK / 2 + dN * dK / 2 + (dM + dN) * dK / 32 + 2 * dM * dN
     dgbs = dbytes / (dr["avg_us"] * 1e-6) / 1e9
-    return {"workload": "mxfp4_gemm_decode_%dx%dx%d" % (dM, dN, dK), "value": round(dgbs, 1),
+    wl = "mxfp4_gemm_decode_%dx%dx%d" % (dM, dN, dK)
+    return {"workload": wl, "value": round(dgbs, 1),
             "unit": "GB/s", "kernel": dr["cfg"].knl_name, "kernel_avg_us": round(dr["avg_us"], 2),
             "frac_hbm": round(dgbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(dbytes),
-            "weight_sets": 3}
+            "weight_sets": 3,
+            "roofline": roofline(wl, dgbs, "hbm", HBM_PEAK_GBS, "GB/s", dr["cfg"].knl_name,
+                                 dr["ld"].log2_k_split)}
 
 
 def settle_first_run(torch, f4gemm, a, bs, M, N, K, warmup, elem_bits=8):
@@ -567,29 +574,46 @@ def deepseek_legs(torch, ops, opus_gemm, steps, warmup):
     return out
 
 
-# Workloads a counter run can isolate: name -> (kind, M, N, K, log2_k_split).
-# The decode entries carry the split the decode leg reports for the shape.
+# Workloads a counter run can isolate, under the names of the bench entries
+# whose roofline they fill: name -> (kind, M, N, K, log2_k_split). The decode
+# entries take the heuristic's split (-1), the split the decode leg reports.
+# Kinds: mx / mxd / mx4 / mx4d MX GEMMs (d: decode data), bs / bs16 block
+# scale on N(0,1) data with fp32 / bf16 C, bsr block scale on the reference
+# driver's data, pt per-tensor, q_<quantiser>_<f32|bf16> the quantisers on an
+# M x K input.
 PROFILE_WORKLOADS = {
     "mxfp8_gemm_8192x8192x8192": ("mx", 8192, 8192, 8192, 0),
     "mxfp8_gemm_4096x4096x4096": ("mx", 4096, 4096, 4096, 0),
-    "mxfp8_gemm_decode_16x28672x8192": ("mxd", 16, 28672, 8192, 0),
-    "mxfp8_gemm_decode_16x8192x28672": ("mxd", 16, 8192, 28672, 0),
-    "mxfp8_gemm_decode_1x28672x8192": ("mxd", 1, 28672, 8192, 0),
-    "mxfp8_gemm_decode_1x8192x28672": ("mxd", 1, 8192, 28672, 0),
-    "mxfp8_gemm_decode_64x28672x8192": ("mxd", 64, 28672, 8192, 0),
-    "mxfp8_gemm_decode_64x8192x28672": ("mxd", 64, 8192, 28672, 2),
+    "mxfp8_gemm_decode_16x28672x8192": ("mxd", 16, 28672, 8192, -1),
+    "mxfp8_gemm_decode_16x8192x28672": ("mxd", 16, 8192, 28672, -1),
+    "mxfp8_gemm_decode_1x28672x8192": ("mxd", 1, 28672, 8192, -1),
+    "mxfp8_gemm_decode_1x8192x28672": ("mxd", 1, 8192, 28672, -1),
+    "mxfp8_gemm_decode_64x28672x8192": ("mxd", 64, 28672, 8192, -1),
+    "mxfp8_gemm_decode_64x8192x28672": ("mxd", 64, 8192, 28672, -1),
     "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out": ("bs", 8192, 8192, 8192, 0),
+    "fp8_blockscale_1x128_128x128_8192x8192x8192_f32out_refdata": ("bsr", 8192, 8192, 8192, 0),
     "fp8_per_tensor_8192x8192x8192_bf16out": ("pt", 8192, 8192, 8192, 0),
-    "fp8_blockscale_deepseek_4096x7168x2048": ("bs", 4096, 7168, 2048, 0),
-    "fp8_blockscale_deepseek_4096x2112x7168": ("bs", 4096, 2112, 7168, 0),
-    "fp8_blockscale_deepseek_4096x24576x1536": ("bs", 4096, 24576, 1536, 0),
     "mxfp4_gemm_8192x8192x8192": ("mx4", 8192, 8192, 8192, 0),
+    "mxfp4_gemm_decode_16x28672x8192": ("mx4d", 16, 28672, 8192, 0),
 }
+for _m, _n, _k in ((4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)):
+    PROFILE_WORKLOADS["fp8_blockscale_deepseek_%dx%dx%d_f32out" % (_m, _n, _k)] = (
+        "bs", _m, _n, _k, 0)
+    PROFILE_WORKLOADS["fp8_blockscale_deepseek_%dx%dx%d_bf16out" % (_m, _n, _k)] = (
+        "bs16", _m, _n, _k, 0)
+for _q in ("mxfp8", "mxfp4", "fp8_1x128", "fp8_128x128"):
+    for _t in ("f32", "bf16"):
+        PROFILE_WORKLOADS["quant_%s_8192x8192_%s" % (_q, _t)] = ("q_%s_%s" % (_q, _t), 8192, 0,
+                                                                 8192, 0)
 
 # Library kernels a workload's calls launch (the GEMM and, for split-K, the
 # reduce); the quantisers and torch's set-up kernels are not part of a call.
-def _call_kernel(name):
-    return name.startswith("void ga::") and "quant" not in name
+def _call_kernel(name, quant=False):
+    """A library dispatch of the profiled call: the quantiser for a quantiser
+    workload, else the GEMM (and its reduce), not the set-up's quantisers."""
+    if not name.startswith("void ga::"):
+        return False
+    return ("quant" in name or "amax" in name) == quant
 
 
 def _mx_choice(f4gemm, M, N, K, l2, eb):
@@ -605,10 +629,13 @@ def profile_workload(torch, name, calls):
     counter run's dispatches after the set-up are exactly those calls)."""
     from gcnasm_amd import f4gemm, opus_gemm, ops
     kind, M, N, K, l2 = PROFILE_WORKLOADS[name]
-    if kind in ("mx", "mxd", "mx4"):
-        eb = 4 if kind == "mx4" else 8
-        a, bs = mx_problem(torch, ops, f4gemm, M, N, K, b_std=0.02 if kind == "mxd" else 1.0,
-                           nsets=3 if kind == "mxd" else 1, seed=1, elem_bits=eb)
+    if kind.startswith("q_"):
+        return _profile_quant(torch, kind, M, K, calls)
+    if kind in ("mx", "mxd", "mx4", "mx4d"):
+        eb = 4 if kind in ("mx4", "mx4d") else 8
+        dec = kind in ("mxd", "mx4d")
+        a, bs = mx_problem(torch, ops, f4gemm, M, N, K, b_std=0.02 if dec else 1.0,
+                           nsets=3 if dec else 1, seed=1, elem_bits=eb)
         sh = f4gemm.Shape(M, N, K, elem_bits=eb)
         cfg, l2 = _mx_choice(f4gemm, M, N, K, l2, eb)
         ld = f4gemm.make_launch(cfg, M, N, K, l2)
@@ -623,16 +650,21 @@ def profile_workload(torch, name, calls):
             kern.launch(args[i % len(args)], ld.gdx, ld.gdy, ld.gdz, workspace=ws)
         info = {"kernel": cfg.knl_name, "log2_k_split": ld.log2_k_split}
     else:
-        xa, xb = scaled_inputs(torch, M, N, K, seed=17)
-        if kind == "pt":
-            qa, sa = ops.quant_fp8_per_tensor(xa)
-            qb, sb = ops.quant_fp8_per_tensor(xb)
-            c, gn = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0"), 0
-        else:
-            qa, sa = ops.quant_fp8_1x128(xa)
-            qb, sb = ops.quant_fp8_128x128(xb)
+        if kind == "bsr":
+            qa, qb, sa, sb = ref_bs_operands(torch, M, 7)
             c, gn = torch.empty((M, N), dtype=torch.float32, device="cuda:0"), 128
-        del xa, xb
+        else:
+            xa, xb = scaled_inputs(torch, M, N, K, seed=17)
+            if kind == "pt":
+                qa, sa = ops.quant_fp8_per_tensor(xa)
+                qb, sb = ops.quant_fp8_per_tensor(xb)
+                c, gn = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0"), 0
+            else:
+                qa, sa = ops.quant_fp8_1x128(xa)
+                qb, sb = ops.quant_fp8_128x128(xb)
+                cdt = torch.bfloat16 if kind == "bs16" else torch.float32
+                c, gn = torch.empty((M, N), dtype=cdt, device="cuda:0"), 128
+            del xa, xb
         ka = opus_gemm.make_kargs(qa, qb, c, sa, sb, M, N, K, 1, gn)
         out = opus_gemm._out_dtype(c)
         torch.cuda.synchronize()
@@ -644,6 +676,36 @@ def profile_workload(torch, name, calls):
         info = {"kernel": "fp8_gemm" if gn == 0 else "gemm_a8w8_blockscale", "log2_k_split": 0}
     torch.cuda.synchronize()
     return info
+
+
+def _profile_quant(torch, kind, M, K, calls):
+    """Counter run of one quantiser on an M x K fp32 or bf16 input (the
+    quantiser legs' call through the C ABI)."""
+    from gcnasm_amd import _lib
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    sh = torch.cuda.current_stream().cuda_stream
+    qname, dt = kind[2:].rsplit("_", 1)
+    code = _lib.GA_IN_F32 if dt == "f32" else _lib.GA_IN_BF16
+    x = torch.randn((M, K), device=dev).to(torch.float32 if dt == "f32" else torch.bfloat16)
+    q = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    s = torch.empty((M * K // 32,), dtype=torch.float32, device=dev)
+    calls_ = {
+        "mxfp8": lambda: lib.ga_quant_mxfp8(x.data_ptr(), code, M, K, K, q.data_ptr(), K,
+                                            s.data_ptr(), K // 32, 0, sh),
+        "mxfp4": lambda: lib.ga_quant_mxfp4(x.data_ptr(), code, M, K, K, q.data_ptr(), K // 2,
+                                            s.data_ptr(), K // 32, 0, sh),
+        "fp8_1x128": lambda: lib.ga_quant_fp8_1x128(x.data_ptr(), code, M, K, K, q.data_ptr(),
+                                                    K, s.data_ptr(), M, sh),
+        "fp8_128x128": lambda: lib.ga_quant_fp8_128x128(x.data_ptr(), code, M, K, K,
+                                                        q.data_ptr(), K, s.data_ptr(),
+                                                        K // 128, sh)}
+    fn = calls_[qname]
+    torch.cuda.synchronize()
+    for _ in range(calls):
+        _lib.check(fn())
+    torch.cuda.synchronize()
+    return {"kernel": "ga_quant_" + qname, "log2_k_split": 0}
 
 
 def traffic_summary(root_dir, calls):
@@ -673,7 +735,8 @@ def traffic_summary(root_dir, calls):
                 d[1] += float(r["Counter_Value"])
             seq = [byd[k] for k in sorted(byd)]
             copies = [v for n, v in seq if "copyBuffer" in n][:2]
-            calls_kib = [v for n, v in seq if _call_kernel(n)]
+            quant = PROFILE_WORKLOADS[wl][0].startswith("q_")
+            calls_kib = [v for n, v in seq if _call_kernel(n, quant)]
             if len(copies) < 2 or not calls_kib:
                 break
             factor = (512 * 1024.0) / (sum(copies) / len(copies))
@@ -682,9 +745,10 @@ def traffic_summary(root_dir, calls):
         if len(per) == 2:
             kind, M, N, K, l2 = PROFILE_WORKLOADS[wl]
             kernel = None
-            if kind in ("mx", "mxd", "mx4"):
+            if kind in ("mx", "mxd", "mx4", "mx4d"):
                 from gcnasm_amd import f4gemm
-                kernel = _mx_choice(f4gemm, M, N, K, l2, 4 if kind == "mx4" else 8)[0].knl_name
+                cfg, l2 = _mx_choice(f4gemm, M, N, K, l2, 4 if kind in ("mx4", "mx4d") else 8)
+                kernel = cfg.knl_name
             res[wl] = {"kernel": kernel,
                        "bytes_per_launch": int(per["FETCH_SIZE"]["bytes_per_call"] +
                                                per["WRITE_SIZE"]["bytes_per_call"]),
@@ -693,6 +757,7 @@ def traffic_summary(root_dir, calls):
                        "fetch_factor": per["FETCH_SIZE"]["factor"],
                        "write_factor": per["WRITE_SIZE"]["factor"],
                        "log2_k_split": l2, "calls": calls,
+                       "dispatches": per["FETCH_SIZE"]["dispatches"],
                        "command": "rocprofv3 --pmc {FETCH_SIZE|WRITE_SIZE} --output-format csv "
                                   "-- python3 bench.py --calib-copy --profile-workload %s "
                                   "--steps %d" % (wl, calls)}
