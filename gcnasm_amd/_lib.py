@@ -211,6 +211,7 @@ SIGNATURES = {
     "ga_blockscale_k_slices": (_i, [ctypes.POINTER(OpusGemmKargs), ctypes.POINTER(_i)]),
     "ga_gemm_a8w8_blockscale_ws": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _i, _vp, _sz, _vp]),
     "ga_blockscale_workspace_bytes": (_i, [ctypes.POINTER(OpusGemmKargs), ctypes.POINTER(_sz)]),
+    "ga_blockscale_workspace_check": (_i, [ctypes.POINTER(OpusGemmKargs), _vp, _sz, _vp]),
     "ga_blockscale_stream_k": (_i, [ctypes.POINTER(OpusGemmKargs), ctypes.POINTER(_i)]),
     "ga_fp8_gemm_per_tensor": (_i, [ctypes.POINTER(OpusGemmKargs), _i, _vp]),
     "ga_splitk_reduce": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _vp]),

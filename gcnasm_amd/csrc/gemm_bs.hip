@@ -455,6 +455,36 @@ ga_status ga_gemm_a8w8_blockscale_ws(const ga_opus_gemm_kargs* kargs, int group_
     return ga_gemm_a8w8_blockscale(kargs, group_n, out_dtype, stream);
 }
 
+ga_status ga_blockscale_workspace_check(const ga_opus_gemm_kargs* kargs, void* workspace,
+                                       size_t workspace_bytes, void* stream)
+{
+    if (!kargs)
+        return fail(GA_ERR_ARG, "blockscale_workspace_check: null kargs");
+    int nwg = 0;
+    ga_status st = bs_stream_k_plan(*kargs, &nwg);
+    if (st != GA_OK || nwg == 0 || !workspace)
+        return st;
+    const size_t counters = bs_sk_counter_bytes(*kargs);
+    if (workspace_bytes < counters)
+        return fail(GA_ERR_WORKSPACE, "blockscale workspace holds %zu bytes, need %zu",
+                    workspace_bytes, counters);
+    hipStream_t s = (hipStream_t)stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    GA_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(GA_ERR_ARG, "blockscale_workspace_check synchronises: not under capture");
+    const size_t tiles = (size_t)((kargs->n + 255) / 256) * ((kargs->m + 255) / 256);
+    unsigned misuse = 0;
+    GA_HIP_CHECK(hipStreamSynchronize(s));
+    GA_HIP_CHECK(hipMemcpy(&misuse, (const char*)workspace + tiles * 4, 4, hipMemcpyDeviceToHost));
+    if (misuse == 0)
+        return GA_OK;
+    GA_HIP_CHECK(hipMemset(workspace, 0, counters));
+    return fail(GA_ERR_WORKSPACE, "blockscale stream-K workspace was not zero-filled before a "
+                                  "call (its tile counters did not start at zero, so some tiles "
+                                  "of that call were not summed); counters cleared");
+}
+
 ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_per_slice)
 {
     if (!kargs || !groups_per_slice)

@@ -32,7 +32,8 @@ struct BsSkArgs {
     int groups;           // K / 128
     int total;            // tiles * groups
     int nwg;              // workgroups (a multiple of 8)
-    unsigned* cnt;        // per-tile arrival counters, zero between calls
+    unsigned* cnt;        // per-tile arrival counters, zero between calls; then
+                          // the misuse word (set when a count ran past its tile's pieces)
     float* part;          // 2 * nwg partial tiles of 65536 floats
 };
 
@@ -450,10 +451,19 @@ __device__ __forceinline__ void sk_segment(int& it, char* smem, int wave)
         // last: when every other piece is already counted, its workgroup
         // finishes the tile from its registers without writing them out.
         bool regs = false;
+        // A count above hi - lo means the counter did not start at zero (the
+        // workspace was not left zero-filled): the tile's sum is lost, and the
+        // misuse word after the counters says so (ga_blockscale_workspace_check).
+        const unsigned* misuse_at = a.cnt + a.tiles_x * a.tiles_y;
         if (v == lo) {
-            if (threadIdx.x == 0)
-                *s_arrived =
+            if (threadIdx.x == 0) {
+                const unsigned seen =
                     __hip_atomic_load(a.cnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (seen > (unsigned)(hi - lo))
+                    __hip_atomic_store((unsigned*)misuse_at, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                *s_arrived = seen;
+            }
             barrier_lds();
             regs = __builtin_amdgcn_readfirstlane(*s_arrived) == (unsigned)(hi - lo);
             barrier_lds(); // read in every wave before the word is written again
@@ -472,6 +482,9 @@ __device__ __forceinline__ void sk_segment(int& it, char* smem, int wave)
                                                             __HIP_MEMORY_SCOPE_AGENT);
                 if (old == (unsigned)(hi - lo))
                     __hip_atomic_store(a.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else if (old > (unsigned)(hi - lo))
+                    __hip_atomic_store((unsigned*)misuse_at, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
                 *s_arrived = old;
             }
             barrier_lds();
@@ -573,10 +586,11 @@ int bs_sk_workgroups(const ga_opus_gemm_kargs& ka, int num_cu)
     return nwg;
 }
 
+// One arrival counter per tile, then the misuse word, rounded to 256 bytes.
 size_t bs_sk_counter_bytes(const ga_opus_gemm_kargs& ka)
 {
     const size_t tiles = (size_t)((ka.n + 255) / 256) * ((ka.m + 255) / 256);
-    return (tiles * 4 + 255) / 256 * 256;
+    return ((tiles + 1) * 4 + 255) / 256 * 256;
 }
 
 size_t bs_sk_workspace_bytes(const ga_opus_gemm_kargs& ka, int nwg)

@@ -735,12 +735,40 @@ const MxKernel* mx_registry_get(int idx)
     return &g_named[idx - kStaticCount];
 }
 
-template <bool BPS, bool FP4>
-static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
-                            int gdx, int gdy, int gdz, hipStream_t stream)
+// The tile a by-name entry runs for a shape, remembered per (B layout,
+// element width, M, N, K, log2 split, CU count) in a small direct-mapped
+// table, so that repeated launches of one shape do not repeat the selection.
+struct ShapePick {
+    int key[7];
+    int idx;
+    bool valid;
+};
+
+template <typename F>
+static int picked_tile(const int (&key)[7], F select)
 {
-    (void)gdx;
-    (void)gdy;
+    static std::mutex mu;
+    static ShapePick table[64];
+    uint32_t h = 2166136261u;
+    for (int v : key)
+        h = (h ^ (uint32_t)v) * 16777619u;
+    ShapePick& e = table[h % 64];
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (e.valid && memcmp(e.key, key, sizeof(e.key)) == 0)
+            return e.idx;
+    }
+    const int idx = select();
+    std::lock_guard<std::mutex> lock(mu);
+    memcpy(e.key, key, sizeof(e.key));
+    e.idx = idx;
+    e.valid = true;
+    return idx;
+}
+
+template <bool BPS, bool FP4>
+static int select_by_shape(const ga_f4gemm_kargs& args, int L, int num_cu)
+{
     const int first = FP4 ? kMx4First : 0, count = FP4 ? kMx4Count : kManifestCount;
     ga_tile_config table[kManifestCount];
     int map[kManifestCount], n = 0;
@@ -749,11 +777,7 @@ static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_spl
             map[n] = i;
             table[n++] = g_mx_kernels[i].cfg;
         }
-    int num_cu = 0;
-    if (device_cu_count(&num_cu) != GA_OK || num_cu <= 0)
-        num_cu = 256;
     int row = -1, l2 = 0;
-    const int L = gdz > 1 ? args.log2_k_split : 0;
     int idx = map[0]; // the 256x256 tile of this width takes any shape
     if (!BPS)
         for (int i = 0; i < n; i++)
@@ -763,6 +787,21 @@ static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_spl
                          &row, &l2) == GA_OK &&
         row >= 0)
         idx = map[row];
+    return idx;
+}
+
+template <bool BPS, bool FP4>
+static void launch_by_shape(const ga_f4gemm_kargs& args, float* ws, const ga_splitk_ws_handle* wsh,
+                            int gdx, int gdy, int gdz, hipStream_t stream)
+{
+    (void)gdx;
+    (void)gdy;
+    int num_cu = 0;
+    if (device_cu_count(&num_cu) != GA_OK || num_cu <= 0)
+        num_cu = 256;
+    const int L = gdz > 1 ? args.log2_k_split : 0;
+    const int key[7] = {BPS ? 1 : 0, FP4 ? 1 : 0, (int)args.M, (int)args.N, (int)args.K, L, num_cu};
+    const int idx = picked_tile(key, [&] { return select_by_shape<BPS, FP4>(args, L, num_cu); });
     const MxKernel& k = g_mx_kernels[idx];
     k.launch(args, ws, wsh, ((int)args.N + k.cfg.tile_N - 1) / k.cfg.tile_N,
              ((int)args.M + k.cfg.tile_M - 1) / k.cfg.tile_M, gdz, stream);

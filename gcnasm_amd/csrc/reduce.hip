@@ -119,10 +119,13 @@ __device__ __forceinline__ void reduce_row(const ReduceArgs& a, const float* ws,
     const int nv = min(8, a.N - n_base);
     // eight outputs in one 16-byte (bf16) or two 16-byte (fp32) stores when
     // the row offset and the pointers allow
+    // (c_in is bf16 whatever the output: its 16-byte read needs the offset
+    // aligned in bf16 elements too)
     const size_t esz = OUT_DTYPE == GA_DTYPE_BF16 ? 2 : 4;
     const bool vout = nv == 8 && ((orow + n_base) * esz) % 16 == 0 &&
                       ((uintptr_t)a.out & 15) == 0 &&
-                      (!a.c_in || ((uintptr_t)a.c_in & 15) == 0);
+                      (!a.c_in || (((uintptr_t)a.c_in & 15) == 0 &&
+                                   ((orow + n_base) * 2) % 16 == 0));
     if (vout) {
         float v[8];
         uint4 cbits = make_uint4(0, 0, 0, 0);

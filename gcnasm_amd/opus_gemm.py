@@ -67,6 +67,16 @@ def gemm_a8w8_blockscale(kargs, out_dtype, group_n=128, stream=None, workspace=N
                                            _stream_handle(stream)))
 
 
+def workspace_check(kargs, workspace, stream=None):
+    """ga_blockscale_workspace_check: raises (GA_ERR_WORKSPACE) when a
+    stream-K call on `workspace` found its tile counters not zero-filled, and
+    zero-fills them again; waits for the stream."""
+    check(lib().ga_blockscale_workspace_check(ctypes.byref(kargs),
+                                              ctypes.c_void_p(workspace.data_ptr()),
+                                              workspace.numel() * workspace.element_size(),
+                                              _stream_handle(stream)))
+
+
 def workspace_bytes(kargs):
     """Bytes ga_gemm_a8w8_blockscale_ws can use for these kargs (0: none)."""
     n = ctypes.c_size_t(0)

@@ -446,6 +446,18 @@ ga_status ga_gemm_a8w8_blockscale_ws(const ga_opus_gemm_kargs* kargs, int group_
  * current device (0: it runs the whole-tile kernel). */
 ga_status ga_blockscale_workspace_bytes(const ga_opus_gemm_kargs* kargs, size_t* bytes);
 
+/* No counterpart in the reference (whose cross-workgroup counter has no
+ * misuse report). Reports whether a stream-K call of
+ * ga_gemm_a8w8_blockscale_ws on this workspace found a tile counter that had
+ * not started at zero (a workspace not zero-filled, e.g. reused for other
+ * data, or shared by overlapping calls): such a call leaves some of its tiles
+ * unsummed, and the kernel records it in a word after the counters. Waits for
+ * the stream, then returns GA_OK, or GA_ERR_WORKSPACE after zero-filling the
+ * counters and the word again. GA_OK at once when these kargs take no
+ * stream-K plan or workspace is NULL; GA_ERR_ARG under stream capture. */
+ga_status ga_blockscale_workspace_check(const ga_opus_gemm_kargs* kargs, void* workspace,
+                                        size_t workspace_bytes, void* stream);
+
 /* Stream-K plan of ga_gemm_a8w8_blockscale_ws (given a workspace) on the
  * current device: *workgroups = P, or 0 when that call runs whole tiles.
  * With G = K/128 and T = tiles * G, iteration t*G + g is 128-K group g of

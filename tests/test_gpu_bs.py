@@ -17,7 +17,7 @@ import torch
 
 import oracle
 from gcnasm_amd import opus_gemm, ops
-from helpers import assert_parity, bf16_compare, f32_compare, tile_rows
+from helpers import assert_parity, bf16_compare, f32_compare, mx_operands, tile_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -272,16 +272,88 @@ def test_blockscale_stream_k(dev, group_n, shape):
         print("stream-K %s group_n=%d %s P=%d" % (shape, group_n, dt, P), flush=True)
         C = run_bs_ws(dev, qa, qb, sfa, sfb, dt, group_n, ws)
         C2 = run_bs_ws(dev, qa, qb, sfa, sfb, dt, group_n, ws)
+        whole = run_bs_ws(dev, qa, qb, sfa, sfb, dt, group_n, None)
         if dt == torch.float32:
             got = C.cpu().numpy()
             ok, st = f32_compare(got[rows], want, absdot=absdot)
             np.testing.assert_array_equal(C2.cpu().numpy().view(np.uint32), got.view(np.uint32))
+            g64, w64 = got.astype(np.float64), whole.cpu().numpy().astype(np.float64)
         else:
             got = C.view(torch.int16).cpu().numpy().view(np.uint16)
             ok, st = bf16_compare(got[rows], oracle.to_bf16_bits(want), absdot)
             np.testing.assert_array_equal(C2.view(torch.int16).cpu().numpy(), got.view(np.int16))
+            g64 = oracle.bf16_bits_to_f32(got).astype(np.float64)
+            w64 = oracle.bf16_bits_to_f32(
+                whole.view(torch.int16).cpu().numpy().view(np.uint16)).astype(np.float64)
         assert_parity(st, "stream-K %s g%d %s" % (shape, group_n, dt))
+        # every output against the whole-tile kernel's: the two differ only
+        # in where a tile's K chain is cut (fp32 rounding of the pieces' sum,
+        # far below 2^-14 of the row's largest output; a bf16 output may also
+        # round to the neighbouring code), so a partial slot or quadrant
+        # mixed up anywhere in a cut tile shows
+        tol = 2.0 ** -14 * np.abs(w64).max(axis=1, keepdims=True)
+        if dt == torch.bfloat16:
+            tol = tol + np.abs(w64) * 2.0 ** -7
+        far = np.abs(g64 - w64) > tol
+        print("stream-K %s g%d %s against the whole-tile kernel: %d of %d outputs differ, "
+              "%d beyond the bound" % (shape, group_n, dt, int((g64 != w64).sum()), g64.size,
+                                       int(far.sum())), flush=True)
+        assert not far.any()
     assert int(ws[:((M + 255) // 256) * ((N + 255) // 256) * 4].sum()) == 0, "counters not reset"
+
+
+def test_blockscale_stream_k_reports_a_dirty_workspace(dev):
+    """A workspace first used as an MX split-K workspace (fp32 partials where
+    the tile counters live) and then given to a stream-K call without
+    zero-filling it: the call's misuse is reported by
+    ga_blockscale_workspace_check, which zero-fills the counters again, and
+    the next stream-K call on it is right (the whole-tile kernel's result
+    within the cut's fp32 rounding) and leaves it clean."""
+    from gcnasm_amd import _lib, f4gemm
+    from gcnasm_amd._lib import GaError
+    M, N, K = 2048, 2560, 8192
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=91)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ka = opus_gemm.make_kargs(t(qa[0][None]), t(qb[0][None]), C, t(sfa[0][None]),
+                              t(sfb[0][None]), M, N, K, 1, 128)
+    nbytes = opus_gemm.workspace_bytes(ka)
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    # an MX split-K GEMM writes its fp32 partials from the workspace's start
+    mM, mN, mK, l2 = 256, 1024, 4096, 2
+    mqa, msa, mqb, msb = mx_operands(mM, mN, mK, seed=92)
+    cfg = [c for c in f4gemm.manifest() if c.knl_name == "ga_mxfp8_bf16_BpreShuffle_256x256_splitK"][0]
+    sh = f4gemm.Shape(mM, mN, mK)
+    D = torch.empty((sh.d_rows_pad(), mN), dtype=torch.bfloat16, device=dev)
+    a_pad = np.zeros((sh.a_rows_pad(), mK), dtype=np.uint8)
+    a_pad[:mM] = mqa
+    bufs = [t(a_pad), t(f4gemm.shuffle_weight_16x16(mqb, mN, mK)),
+            t(f4gemm.shuffle_scale(msa, mM, mK // 32, sh.scale_a_rows(), sh.scale_cols())),
+            t(f4gemm.shuffle_scale(msb, mN, mK // 32, sh.scale_b_rows(), sh.scale_cols()))]
+    ld = f4gemm.make_launch(cfg, mM, mN, mK, l2)
+    args = f4gemm.fill_args(D, None, *bufs, mM, mN, mK, mN, sh.scale_cols(), sh.scale_cols(),
+                            1.0, 0.0, ld.log2_k_split)
+    ws32 = ws.view(torch.float32)
+    assert ld.gdz * mM * mN <= ws32.numel()
+    f4gemm.Kernel().load(None, cfg).launch(args, ld.gdx, ld.gdy, ld.gdz, workspace=ws32)
+    torch.cuda.synchronize()
+    assert int((ws[:64] != 0).sum()) > 0, "the MX partials should leave the counters dirty"
+    whole = run_bs_ws(dev, qa[0], qb[0], sfa[0], sfb[0], torch.float32, 128, None)
+    opus_gemm.gemm_a8w8_blockscale(ka, _lib.GA_DTYPE_F32, 128, workspace=ws)
+    with pytest.raises(GaError) as e:
+        opus_gemm.workspace_check(ka, ws)
+    assert e.value.status == _lib.GA_ERR_WORKSPACE
+    print("dirty workspace reported: %s" % e.value, flush=True)
+    C.fill_(float("nan"))
+    opus_gemm.gemm_a8w8_blockscale(ka, _lib.GA_DTYPE_F32, 128, workspace=ws)
+    opus_gemm.workspace_check(ka, ws)
+    got = C.cpu().numpy().astype(np.float64)
+    w64 = whole.cpu().numpy().astype(np.float64)
+    tol = 2.0 ** -14 * np.abs(w64).max(axis=1, keepdims=True)
+    assert not np.any(np.abs(got - w64) > tol)
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    assert int(ws[:(tiles + 1) * 4].sum()) == 0, "counters and misuse word left zero"
 
 
 def test_blockscale_ws_whole_tiles_where_they_fit():

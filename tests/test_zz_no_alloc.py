@@ -77,3 +77,43 @@ def test_noalloc_rejects_partials_beyond_the_scratch(dev):
                                       None)
     assert st == _lib.GA_ERR_WORKSPACE
     torch.cuda.synchronize()
+
+
+def test_noalloc_under_graph_capture(dev):
+    """ga_kernel_launch_noalloc captured into a HIP graph (global capture
+    mode, in which the library-owned workspace path is refused) and replayed:
+    every replay gives the eager caller-workspace launch's bits, with other
+    no-alloc calls (a smaller problem, which rewrites the scratch array)
+    between the replays."""
+    lib = _lib.lib()
+    name = "ga_mxfp8_bf16_BpreShuffle_256x256_splitK"
+    M, N, K, l2 = 256, 1024, 4096, 2
+    idx, ld, outs, bufs = _problem(dev, M, N, K, name, l2, 7)
+    (D0, a0), (D1, a1) = outs
+    ws = torch.empty(ld.gdz * M * N, dtype=torch.float32, device=dev)
+    _lib.check(lib.ga_kernel_launch(idx, ctypes.byref(a0), ld.gdx, ld.gdy, ld.gdz,
+                                    ws.data_ptr(), ws.numel() * 4, None))
+    # the eager no-alloc call first: the scratch array's address is looked up
+    # outside capture
+    _lib.check(lib.ga_kernel_launch_noalloc(idx, ctypes.byref(a1), ld.gdx, ld.gdy, ld.gdz, None))
+    torch.cuda.synchronize()
+    want = _bits(D0, M)
+    np.testing.assert_array_equal(_bits(D1, M), want)
+    sidx, sld, souts, sbufs = _problem(dev, 128, 512, 2048, name, 1, 8)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        _lib.check(lib.ga_kernel_launch_noalloc(idx, ctypes.byref(a1), ld.gdx, ld.gdy, ld.gdz,
+                                                ctypes.c_void_p(s.cuda_stream)))
+    for rep in range(4):
+        D1.fill_(float("nan"))
+        torch.cuda.synchronize()
+        print("noalloc graph replay %d" % rep, flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_bits(D1, M), want, err_msg="replay %d" % rep)
+        _lib.check(lib.ga_kernel_launch_noalloc(sidx, ctypes.byref(souts[0][1]), sld.gdx, sld.gdy,
+                                                sld.gdz, None))
+        torch.cuda.synchronize()
+    del g, ws, outs, bufs, souts, sbufs
