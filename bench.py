@@ -595,6 +595,9 @@ PROFILE_WORKLOADS = {
     "fp8_per_tensor_8192x8192x8192_bf16out": ("pt", 8192, 8192, 8192, 0),
     "mxfp4_gemm_8192x8192x8192": ("mx4", 8192, 8192, 8192, 0),
     "mxfp4_gemm_decode_16x28672x8192": ("mx4d", 16, 28672, 8192, 0),
+    # the MFMA-only probe on the 8192^3 problem's A bytes (a clock reference
+    # for counter runs: it reports the shader clock it measured in-kernel)
+    "mfma_probe": ("probe", 8192, 8192, 8192, 0),
 }
 for _m, _n, _k in ((4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)):
     PROFILE_WORKLOADS["fp8_blockscale_deepseek_%dx%dx%d_f32out" % (_m, _n, _k)] = (
@@ -631,6 +634,13 @@ def profile_workload(torch, name, calls):
     kind, M, N, K, l2 = PROFILE_WORKLOADS[name]
     if kind.startswith("q_"):
         return _profile_quant(torch, kind, M, K, calls)
+    if kind == "probe":
+        a, bs = mx_problem(torch, ops, f4gemm, M, N, K)
+        del bs
+        torch.cuda.synchronize()
+        info = mfma_ceiling(torch, a.codes)
+        torch.cuda.synchronize()
+        return {"kernel": "probe_mfma_kernel", "log2_k_split": 0, **(info or {})}
     if kind in ("mx", "mxd", "mx4", "mx4d"):
         eb = 4 if kind in ("mx4", "mx4d") else 8
         dec = kind in ("mxd", "mx4d")
