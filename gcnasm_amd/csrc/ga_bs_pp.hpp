@@ -132,30 +132,50 @@ __device__ __forceinline__ void apply_scales(const ScaleVals& v, v4f (&acc)[4][2
     }
 }
 
+// The tiles of a quadrant with t = 1 (GROUP_N 128), folded by the memory
+// slot that follows the quadrant's MFMA slot when the fold is split.
+template <int MODE>
+__device__ __forceinline__ void apply_scales_t1(const ScaleVals& v, v4f (&acc)[4][2],
+                                                const v4f (&p)[4][2])
+{
+    static_assert(MODE == PS_GROUP128, "split fold: one SFB value per quadrant");
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float s = v.sa[i] * v.sb0[0];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            acc[i][1][j] = __builtin_fmaf(p[i][1][j], s, acc[i][1][j]);
+    }
+}
+
 // MFMA slot: the quadrant's 8 MFMAs (4 A tiles x 2 B tiles of one 128-K
 // group; unit E8M0 scales). For the block-scale modes each MFMA writes a
 // zeroed temporary p[i][t], and just before it the previous quadrant's
 // p[i][t] is folded into its accumulator (acc += p * SFA*SFB): the VALU work
-// of a tile issues while the MFMA pipe runs the previous tile's MFMA.
-template <int MODE, bool APPLY>
+// of a tile issues while the MFMA pipe runs the previous tile's MFMA. With
+// SPLIT only the t = 0 tiles are folded here; the memory slot before this
+// one folded the t = 1 tiles (BS_MEM_SLOT_SPLIT).
+template <int MODE, bool APPLY, bool SPLIT = false>
 __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], v4f (&p)[4][2], const v8i (&a)[4],
                                              const v8i (&b)[2], v4f (&acc_prev)[4][2],
                                              const ScaleVals& sv)
 {
+    static_assert(!SPLIT || MODE == PS_GROUP128, "split fold: GROUP_N 128 only");
     __builtin_amdgcn_s_setprio(1);
     static_for<4>([&](auto I) {
         constexpr int i = decltype(I)::value;
         static_for<2>([&](auto T) {
             constexpr int t = decltype(T)::value;
+            constexpr bool fold = APPLY && !(SPLIT && t == 1);
             if constexpr (MODE == PS_TENSOR) {
                 acc[i][t] = mfma_mx16<0, 0>(b[t], a[i], acc[i][t], 127, 127);
             } else {
                 // keep the order fold(tile) -> MFMA(tile), tile by tile
-                if constexpr (APPLY)
+                if constexpr (fold)
                     __builtin_amdgcn_sched_group_barrier(
                         0x2, MODE == PS_GROUP128 ? (t == 0 ? 5 : 4) : 8, 0);
                 __builtin_amdgcn_sched_group_barrier(0x8, 1, 0);
-                if constexpr (APPLY) {
+                if constexpr (fold) {
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const float s = MODE == PS_GROUP128 ? sv.sa[i] * sv.sb0[0]
@@ -180,6 +200,27 @@ __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], v4f (&p)[4][2], c
         sv = read_scales<MODE, HMP, HNP>(rb, RING);                                          \
         __builtin_amdgcn_sched_barrier(0);                                                   \
         READS;                                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        phase_sync<WAITN>();                                                                 \
+    }
+
+// Memory slot of the split fold (GROUP_N 128): the scales of quadrant (HM,
+// HN), which the coming MFMA slot computes, are read one memory slot ahead
+// into `svn`; the scales read by the previous memory slot (`sv`) serve this
+// slot's fold of the t = 1 tiles of ACCP, the quadrant the previous MFMA
+// slot computed, after the operand reads, and the coming MFMA slot's fold of
+// its t = 0 tiles. Half of the fold's VALU work so leaves the MFMA slot
+// without delaying the operand reads.
+#define BS_MEM_SLOT_SPLIT(HM, HN, RING, COPIES, READS, WAITN, ACCP, DOFOLD)                  \
+    {                                                                                        \
+        sv = svn;                                                                            \
+        COPIES;                                                                              \
+        svn = read_scales<MODE, HM, HN>(rb, RING);                                           \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        READS;                                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        if (DOFOLD)                                                                          \
+            apply_scales_t1<MODE>(sv, ACCP, p);                                              \
         __builtin_amdgcn_sched_barrier(0);                                                   \
         phase_sync<WAITN>();                                                                 \
     }

@@ -12,9 +12,13 @@
 // slots refilled half tile by half tile. Differences:
 //  * the MFMA runs with unit E8M0 scales into a zeroed temporary (8 tiles x
 //    4 VGPRs); the fp32 scaling of quadrant k is folded into its accumulator
-//    in the NEXT MFMA slot, tile by tile just before the MFMA that reuses the
-//    tile's temporary, so the VALU work issues between MFMAs: s = SFA[m] *
-//    SFB (GROUP_N 1: per column), then four fmaf per tile and lane;
+//    before the next MFMA slot reuses the temporaries: s = SFA[m] * SFB
+//    (GROUP_N 1: per column), then four fmaf per tile and lane. GROUP_N 1
+//    folds every tile in the next MFMA slot, just before the MFMA that
+//    reuses it; GROUP_N 128 splits the fold: the t = 0 tiles there, the
+//    t = 1 tiles in the memory slot between the two MFMA slots, after its
+//    operand reads (the VALU work of a fold placed in the MFMA slot adds to
+//    that slot; half of it in each slot shortens the longer one);
 //  * per K group the scales travel with the operands: SFA[g, m0..m0+255]
 //    (1 KB, copied by waves 0-3, permuted so a lane's four rows are one
 //    16-byte LDS read) and SFB (waves 4-7: the tile's two 128-column blocks,
@@ -48,7 +52,7 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
     const int nsteps = K / 128;
 
     v4f acc[4][4][2];
-    v4f p[4][2]; // MFMA results of the last quadrant, scaled in the next memory slot
+    v4f p[4][2]; // MFMA results of the last quadrant, folded before the next MFMA slot reuses them
 #pragma unroll
     for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -141,9 +145,8 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
     if (grp == 1)
         slot_sync(); // second group runs one barrier behind
 
-    // K group s (LDS slot s & 1, scale ring slot r0). A memory slot first
-    // applies the scales of the quadrant the previous MFMA slot produced,
-    // then issues its copy, then its operand read, then waits:
+    // K group s (LDS slot s & 1, scale ring slot r0). A memory slot issues
+    // its copy, reads scales, then its operand read, then waits:
     //   phase  read      copy            quadrant   younger copies
     //   1      A0(s)     A1(s+1)         00         10 + S
     //   2      B1(s)     B0+S(s+2)       01         10 + 2S
@@ -152,38 +155,82 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
     // The loop's first quadrant has nothing to fold in: peel it.
     // Scale ring slot of group s: s % 4. The copy of group s+2 (phase 2 of
     // group s) overwrites group s-2's slot, last read for the fold in phase 1
-    // of group s-1.
+    // of group s-1 (unsplit fold) or in phase 4 of group s-2 (split).
     ScaleVals sv;
-    for (int s = 0; s < nsteps; s++) {
-        const int slot = s & 1;
-        const int r0 = s & 3, r2 = (s + 2) & 3, rprev = (s - 1) & 3;
-        // phase 1 (folds in quadrant 11 of the previous group)
-        BS_MEM_SLOT(1, 1, rprev, issue_a(L, smem, 1, s + 1, wave), read_a<0>(rb, slot, fa),
-                    10 + S);
-        if (s > 0)
-            mma_quadrant<MODE, true>(acc[0], p, fa, fb0, acc[3], sv);
-        else
-            mma_quadrant<MODE, false>(acc[0], p, fa, fb0, acc[3], sv);
-        slot_sync();
-        // phase 2
-        BS_MEM_SLOT(0, 0, r0,
-                    issue_b(L, smem, 0, s + 2, wave); if (S) issue_s(L, smem, s + 2, r2, wave),
-                    read_b<1>(rb, slot, fb1), 10 + 2 * S);
-        mma_quadrant<MODE, true>(acc[1], p, fa, fb1, acc[0], sv);
-        slot_sync();
-        // phase 3
-        BS_MEM_SLOT(0, 1, r0, issue_a(L, smem, 0, s + 2, wave), read_a<1>(rb, slot, fa), 10 + S);
-        mma_quadrant<MODE, true>(acc[2], p, fa, fb0, acc[1], sv);
-        slot_sync();
-        // phase 4
-        BS_MEM_SLOT(1, 0, r0, issue_b(L, smem, 1, s + 2, wave), read_b<0>(rb, slot ^ 1, fb0),
-                    10 + S);
-        mma_quadrant<MODE, true>(acc[3], p, fa, fb1, acc[2], sv);
-        slot_sync();
-    }
-    if (grp == 0)
-        slot_sync(); // matches the second group's extra barrier
-    {
+    if constexpr (MODE == PS_GROUP128) {
+        // Split fold: each memory slot reads the scales of the quadrant the
+        // coming MFMA slot computes and folds the t = 1 tiles of the quadrant
+        // the previous MFMA slot computed after its operand reads; the MFMA
+        // slot folds the t = 0 tiles between its MFMAs. Phase 1 reads group
+        // s's scales, which landed before A0(s) (copied after them), and the
+        // last read of a ring slot (phase 4 of its group) precedes its
+        // overwrite (phase 2 of the group two later). Same fmaf per tile and
+        // group, in the same order, as the unsplit fold.
+        ScaleVals svn = {};
+        sv = svn;
+        for (int s = 0; s < nsteps; s++) {
+            const int slot = s & 1;
+            const int r0 = s & 3, r2 = (s + 2) & 3;
+            // phase 1 (folds in quadrant 11 of the previous group)
+            BS_MEM_SLOT_SPLIT(0, 0, r0, issue_a(L, smem, 1, s + 1, wave),
+                              read_a<0>(rb, slot, fa), 10 + S, acc[3], s > 0);
+            if (s > 0)
+                mma_quadrant<MODE, true, true>(acc[0], p, fa, fb0, acc[3], sv);
+            else
+                mma_quadrant<MODE, false, true>(acc[0], p, fa, fb0, acc[3], sv);
+            slot_sync();
+            // phase 2
+            BS_MEM_SLOT_SPLIT(0, 1, r0,
+                              issue_b(L, smem, 0, s + 2, wave);
+                              issue_s(L, smem, s + 2, r2, wave), read_b<1>(rb, slot, fb1),
+                              10 + 2 * S, acc[0], true);
+            mma_quadrant<MODE, true, true>(acc[1], p, fa, fb1, acc[0], sv);
+            slot_sync();
+            // phase 3
+            BS_MEM_SLOT_SPLIT(1, 0, r0, issue_a(L, smem, 0, s + 2, wave),
+                              read_a<1>(rb, slot, fa), 10 + S, acc[1], true);
+            mma_quadrant<MODE, true, true>(acc[2], p, fa, fb0, acc[1], sv);
+            slot_sync();
+            // phase 4
+            BS_MEM_SLOT_SPLIT(1, 1, r0, issue_b(L, smem, 1, s + 2, wave),
+                              read_b<0>(rb, slot ^ 1, fb0), 10 + S, acc[2], true);
+            mma_quadrant<MODE, true, true>(acc[3], p, fa, fb1, acc[2], sv);
+            slot_sync();
+        }
+        if (grp == 0)
+            slot_sync(); // matches the second group's extra barrier
+        apply_scales<MODE>(svn, acc[3], p);
+    } else {
+        for (int s = 0; s < nsteps; s++) {
+            const int slot = s & 1;
+            const int r0 = s & 3, r2 = (s + 2) & 3, rprev = (s - 1) & 3;
+            // phase 1 (folds in quadrant 11 of the previous group)
+            BS_MEM_SLOT(1, 1, rprev, issue_a(L, smem, 1, s + 1, wave), read_a<0>(rb, slot, fa),
+                        10 + S);
+            if (s > 0)
+                mma_quadrant<MODE, true>(acc[0], p, fa, fb0, acc[3], sv);
+            else
+                mma_quadrant<MODE, false>(acc[0], p, fa, fb0, acc[3], sv);
+            slot_sync();
+            // phase 2
+            BS_MEM_SLOT(0, 0, r0,
+                        issue_b(L, smem, 0, s + 2, wave); if (S) issue_s(L, smem, s + 2, r2, wave),
+                        read_b<1>(rb, slot, fb1), 10 + 2 * S);
+            mma_quadrant<MODE, true>(acc[1], p, fa, fb1, acc[0], sv);
+            slot_sync();
+            // phase 3
+            BS_MEM_SLOT(0, 1, r0, issue_a(L, smem, 0, s + 2, wave), read_a<1>(rb, slot, fa),
+                        10 + S);
+            mma_quadrant<MODE, true>(acc[2], p, fa, fb0, acc[1], sv);
+            slot_sync();
+            // phase 4
+            BS_MEM_SLOT(1, 0, r0, issue_b(L, smem, 1, s + 2, wave), read_b<0>(rb, slot ^ 1, fb0),
+                        10 + S);
+            mma_quadrant<MODE, true>(acc[3], p, fa, fb1, acc[2], sv);
+            slot_sync();
+        }
+        if (grp == 0)
+            slot_sync(); // matches the second group's extra barrier
         const ScaleVals last = read_scales<MODE, 1, 1>(rb, (nsteps - 1) & 3);
         apply_scales<MODE>(last, acc[3], p);
     }
