@@ -581,6 +581,8 @@ ga_status ga_ws_handle_create(ga_splitk_ws_handle** ws_handle)
     GA_HIP_CHECK(hipMalloc(&slot, sizeof(ga_splitk_ws_handle)));
     const ga_splitk_ws_handle init = {nullptr, 0};
     hipError_t e = hipMemcpy(slot, &init, sizeof(init), hipMemcpyHostToDevice);
+    if (e == hipSuccess) // the slot is written before any stream reads it
+        e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(slot);
         return hip_fail(e, "hipMemcpy(ws slot)");
@@ -607,6 +609,8 @@ ga_status ga_ws_handle_reserve(ga_splitk_ws_handle* ws_handle, size_t bytes)
         GA_HIP_CHECK(hipMalloc(&p, bytes));
         const ga_splitk_ws_handle v = {p, (uint64_t)bytes};
         hipError_t e = hipMemcpy(ws_handle, &v, sizeof(v), hipMemcpyHostToDevice);
+        if (e == hipSuccess) // the slot is written before any stream reads it
+            e = hipDeviceSynchronize();
         if (e != hipSuccess) {
             (void)hipFree(p);
             return hip_fail(e, "hipMemcpy(ws slot)");

@@ -479,7 +479,10 @@ ga_status ga_blockscale_workspace_check(const ga_opus_gemm_kargs* kargs, void* w
     GA_HIP_CHECK(hipMemcpy(&misuse, (const char*)workspace + tiles * 4, 4, hipMemcpyDeviceToHost));
     if (misuse == 0)
         return GA_OK;
-    GA_HIP_CHECK(hipMemset(workspace, 0, counters));
+    // cleared on the caller's stream and waited for: a hipMemset would queue
+    // on the null stream, which does not order against a non-blocking stream
+    GA_HIP_CHECK(hipMemsetAsync(workspace, 0, counters, s));
+    GA_HIP_CHECK(hipStreamSynchronize(s));
     return fail(GA_ERR_WORKSPACE, "blockscale stream-K workspace was not zero-filled before a "
                                   "call (its tile counters did not start at zero, so some tiles "
                                   "of that call were not summed); counters cleared");

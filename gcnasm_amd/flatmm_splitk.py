@@ -65,7 +65,8 @@ def make_kargs(a, b, c, split_k, handle, bias=None, bias_per_batch=False):
 
     a [batch, M, K] or [M, K] bf16, b [batch, N, K] or [N, K] bf16, c [.., M, N]
     bf16; workspace [split_k, batch, round_up(M, 64), round_up(N, 64)] fp32;
-    bias bf16 [N] (or [batch, N] with bias_per_batch).
+    bias bf16 [N] (or [batch, N] with bias_per_batch). The struct keeps the
+    tensors and the handle alive for as long as it lives.
     """
     batch = a.shape[0] if a.dim() == 3 else 1
     m, k = a.shape[-2], a.shape[-1]
@@ -84,6 +85,8 @@ def make_kargs(a, b, c, split_k, handle, bias=None, bias_per_batch=False):
     ka.stride_ws_batch = pm * pn
     ka.stride_c_batch = (c.stride(0) if c is not None and c.dim() == 3 else m * n)
     ka.stride_bias_batch = n if bias_per_batch else 0
+    # the struct holds raw device pointers: keep the tensors alive with it
+    ka._tensors = (a, b, c, bias, handle)
     return ka
 
 

@@ -24,6 +24,7 @@ def make_kargs(a, b, c, sfa, sfb, m, n, k, batch=1, group_n=128):
     a [batch, M, K], b [batch, N, K] E4M3 (uint8 tensors); c [batch, M, N];
     sfa [batch, K/128, M] fp32; sfb [batch, ceil(N/128), K/128] (group_n 128)
     or [batch, K/128, N] (group_n 1). Per-tensor: sfa, sfb one fp32 each.
+    The struct keeps the tensors alive for as long as it lives.
     """
     kg = k // 128
     ka = opus_gemm_kargs()
@@ -41,6 +42,8 @@ def make_kargs(a, b, c, sfa, sfb, m, n, k, batch=1, group_n=128):
         ka.stride_sfa_batch, ka.stride_sfb_batch = m * kg, n * kg
     else:  # per-tensor: one scalar each
         ka.stride_sfa = ka.stride_sfb = ka.stride_sfa_batch = ka.stride_sfb_batch = 0
+    # the struct holds raw device pointers: keep the tensors alive with it
+    ka._tensors = (a, b, c, sfa, sfb)
     return ka
 
 

@@ -434,8 +434,10 @@ ga_status ga_blockscale_k_slices(const ga_opus_gemm_kargs* kargs, int* groups_pe
  * gains). The reference's kernel has no split, and its cross-workgroup
  * counter (wmma_opus_rdna4/opus/opus.hpp:1296-1304) spins, where here nobody
  * waits. workspace: ga_blockscale_workspace_bytes bytes (up to about 128
- * MiB), zero-filled before its first use (hipMemset) and left zero-filled by
- * every call; calls that overlap in time must not share it. workspace NULL,
+ * MiB), zero-filled before its first use (on the call's stream, or waited
+ * for before the call: a hipMemset queues on the null stream, which does not
+ * order against non-blocking streams) and left zero-filled by every call;
+ * calls that overlap in time must not share it. workspace NULL,
  * or a shape the whole-tile kernel suits, runs exactly
  * ga_gemm_a8w8_blockscale; a workspace that is too small is
  * GA_ERR_WORKSPACE. Summation order: ga_blockscale_stream_k. */
@@ -453,7 +455,7 @@ ga_status ga_blockscale_workspace_bytes(const ga_opus_gemm_kargs* kargs, size_t*
  * data, or shared by overlapping calls): such a call leaves some of its tiles
  * unsummed, and the kernel records it in a word after the counters. Waits for
  * the stream, then returns GA_OK, or GA_ERR_WORKSPACE after zero-filling the
- * counters and the word again. GA_OK at once when these kargs take no
+ * counters and the word again on that stream and waiting for it. GA_OK at once when these kargs take no
  * stream-K plan or workspace is NULL; GA_ERR_ARG under stream capture. */
 ga_status ga_blockscale_workspace_check(const ga_opus_gemm_kargs* kargs, void* workspace,
                                         size_t workspace_bytes, void* stream);

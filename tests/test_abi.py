@@ -177,3 +177,32 @@ def test_element_formats_are_validated_without_gpu():
     assert b"e2m1" in l.ga_last_error()
     assert l.ga_kernel_launch_fmt(0, ctypes.byref(args), 99, 1, 1, 1, 1, None, 0, None) == \
         _lib.GA_ERR_ARG
+
+
+def test_kargs_keep_their_tensors_alive():
+    """The kargs structs hold raw device pointers; the Python builders keep
+    the tensors with them, so kargs built from temporaries never point at
+    memory the allocator has handed to something else."""
+    import gc
+    import weakref
+    import torch
+    from gcnasm_amd import flatmm_splitk, opus_gemm
+
+    def build_opus():
+        a, b = torch.zeros((1, 4, 128), dtype=torch.uint8), torch.zeros((1, 4, 128), dtype=torch.uint8)
+        c = torch.zeros((1, 4, 4))
+        sfa, sfb = torch.ones((1, 1, 4)), torch.ones((1, 1, 1))
+        return opus_gemm.make_kargs(a, b, c, sfa, sfb, 4, 4, 128), [weakref.ref(x) for x in (a, b, c, sfa, sfb)]
+
+    def build_flatmm():
+        a, b = torch.zeros((4, 64), dtype=torch.bfloat16), torch.zeros((4, 64), dtype=torch.bfloat16)
+        c = torch.zeros((4, 4), dtype=torch.bfloat16)
+        return flatmm_splitk.make_kargs(a, b, c, 1, None), [weakref.ref(x) for x in (a, b, c)]
+
+    for build in (build_opus, build_flatmm):
+        ka, refs = build()
+        gc.collect()
+        assert all(r() is not None for r in refs)
+        del ka
+        gc.collect()
+        assert all(r() is None for r in refs)
