@@ -574,13 +574,13 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         dec_epilogue<NG, TM>(args, acc, cg0, ng_here, lane);
 }
 
-// Shared-A split variant (33-64 rows). A workgroup of four waves, one per
-// SIMD, takes K slice blockIdx.y of a contiguous range of column groups
-// (nwg equal shares), each wave up to NG of them. Each step's A rows
-// (TM x 16 rows x 128 bytes) go into an LDS ring of D steps with direct-to-LDS
-// loads, 2 * TM / 4 one-KB copies per wave, and every wave reads the whole
-// step from there: a CU reads A once per step for all its columns, and the
-// MFMAs of the 64 rows spread over the four SIMDs. B and the scales stream
+// Shared-A split variant (33-64 rows). A workgroup of W waves (four: one per
+// SIMD; eight: two per SIMD) takes K slice blockIdx.y of a contiguous range
+// of column groups (nwg equal shares), each wave up to NG of them. Each
+// step's A rows (TM x 16 rows x 128 bytes) go into an LDS ring of D steps
+// with direct-to-LDS loads, 2 * TM / W one-KB copies per wave, and every wave
+// reads the whole step from there: a CU reads A once per step for all its
+// columns, and the MFMAs of the 64 rows spread over the four SIMDs. B and the scales stream
 // into registers as in the other variants (ring of D steps per wave).
 // Step u: wait for the wave's loads of step u, barrier (every wave's copies
 // of step u landed, every wave's LDS reads of step u - 1 done), read step u's
@@ -590,9 +590,9 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
 // step, the odd step's operands shifted out during the even step.
 // One slice applies the epilogue; more write fp32 partials for the split-K
 // reduce (ws, or the slot wsh), as the split variant does.
-template <int TM, int NG, bool FP4>
+template <int TM, int NG, bool FP4, int W_ = 4>
 struct LaCfg {
-    static constexpr int W = 4;                       // waves per workgroup
+    static constexpr int W = W_;                      // waves per workgroup
     static constexpr int SA = (TM + 1) / 2;           // A scale dwords per step
     static constexpr int BPW = 2 * TM / W;            // A copies per wave per step
     static constexpr int LB = 2 * NG;                 // B loads per step
@@ -626,12 +626,12 @@ struct LaCfg {
 // (one fp32 chain each, summed in slice order in registers) and apply the
 // epilogue, else gridDim.y == ks and each workgroup writes its slice's
 // partials.
-template <int TM, int NG, bool BPS, bool FP4, int F>
-__global__ __launch_bounds__(256) void mx_decode_la_kernel(ga_f4gemm_kargs args, int nwg, int ks,
+template <int TM, int NG, bool BPS, bool FP4, int F, int W = 4>
+__global__ __launch_bounds__(64 * W) void mx_decode_la_kernel(ga_f4gemm_kargs args, int nwg, int ks,
                                                            float* __restrict__ ws,
                                                            const ga_splitk_ws_handle* __restrict__ wsh)
 {
-    using Cfg = LaCfg<TM, NG, FP4>;
+    using Cfg = LaCfg<TM, NG, FP4, W>;
     constexpr int kEPB = FP4 ? 2 : 1;
     constexpr int D = Cfg::D, SA = Cfg::SA, BPW = Cfg::BPW, kSlot = Cfg::kSlot;
     constexpr bool kPair = Cfg::kPair;
@@ -925,8 +925,11 @@ void launch_dec_xs_ng(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, fl
 }
 
 // Shared-A split variant: nwg workgroups per slice (phys == gdz), or all
-// gdz slices in turn in each workgroup (phys == 1); each wave up to 2 (a
-// share of at most 8 groups) or 4 of its workgroup's groups.
+// gdz slices in turn in each workgroup (phys == 1). A share of at most 8
+// groups runs eight waves of one group each (some without a group), a
+// larger one four waves of up to 4. Measured on MI355X, M = 64, N = 28672,
+// K = 8192 (7 groups per workgroup), best of 3 x 100 calls: 44.0 us against
+// 45.0 us for four waves of 2, 2, 2 and 1 groups (bit-identical outputs).
 template <bool BPS, bool FP4, int F>
 void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int phys, int nwg, float* ws,
                    const ga_splitk_ws_handle* wsh, hipStream_t stream)
@@ -935,7 +938,7 @@ void launch_dec_la(const ga_f4gemm_kargs& args, int gdz, int phys, int nwg, floa
     const int share = (groups + nwg - 1) / nwg;
     const dim3 grid(nwg, phys);
     if (share <= 8)
-        hipLaunchKernelGGL((mx_decode_la_kernel<4, 2, BPS, FP4, F>), grid, dim3(256), 0, stream,
+        hipLaunchKernelGGL((mx_decode_la_kernel<4, 1, BPS, FP4, F, 8>), grid, dim3(512), 0, stream,
                            args, nwg, gdz, ws, wsh);
     else
         hipLaunchKernelGGL((mx_decode_la_kernel<4, 4, BPS, FP4, F>), grid, dim3(256), 0, stream,
@@ -1040,7 +1043,7 @@ int mx_decode_split_groups(const ga_f4gemm_kargs& args, int gdz, int num_cu, int
 namespace {
 
 // Workgroups per slice of the shared-A variant: one per CU over all slices
-// (no more than the groups), at most 16 groups (4 per wave) each.
+// (no more than the groups), at most 16 groups (4 per wave of four) each.
 int la_workgroups(const ga_f4gemm_kargs& args, int gdz, int num_cu)
 {
     const int groups = (int)args.N / 16;
@@ -1064,6 +1067,7 @@ void launch_split_t(const ga_f4gemm_kargs& args, int gdz, int phys, int ng, floa
 {
     if (args.M > 32 && phys == 1 && num_cu > 0)
         launch_dec_la<BPS, FP4, F>(args, gdz, 1, la_workgroups(args, 1, num_cu), ws, wsh, stream);
+
     else if (args.M > 32)
         launch_dec_xs_ng<4, BPS, FP4, F>(args, gdz, phys, ng, ws, wsh, stream);
     else

@@ -381,15 +381,15 @@ def test_decode_split_across_workgroups(dev, M, bps, NKL):
           ("bps" if bps else "plain", M, N, K, ld.gdz), oracle.mx_absdot(qa, sa, qb, sb))
 
 
-# 33-64 rows at one slice over wide N: the shared-A variant (four waves per
-# workgroup, A through an LDS ring). (M, N, K, preshuffled B): 2 groups per
-# wave with the ring (8 steps) longer than the slice (5 steps), 33 rows; 9
-# steps (one pass of the main loop and a one-step tail), waves of 2, 2, 1 and
-# no groups; 4 groups per wave (N > 32768: the five-step ring without paired
-# scale loads) over 13 steps (two passes, a three-step tail) and 9, with one
-# workgroup of 9 groups among 8s.
+# 33-64 rows at one slice over wide N: the shared-A variant (A through an LDS
+# ring). (M, N, K, preshuffled B): eight waves of one group (shares of 6, 5
+# and 7 groups: waves without a group) with the ring (8 steps) longer than the
+# slice (5 steps), 33 rows; 9 steps (one pass of the main loop and a one-step
+# tail); 7 groups per workgroup as at N = 28672; four waves of 4 groups (N >
+# 32768: the five-step ring without paired scale loads) over 13 steps (two
+# passes, a three-step tail) and 9, with one workgroup of 9 groups among 8s.
 SHARED_A_CASES = [(33, 24576, 640, True), (33, 24576, 640, False), (40, 20480, 1152, True),
-                  (64, 32784, 1664, True), (64, 32784, 1152, False)]
+                  (64, 28672, 1152, True), (64, 32784, 1664, True), (64, 32784, 1152, False)]
 
 
 @pytest.mark.parametrize("MNKB", SHARED_A_CASES)

@@ -264,10 +264,11 @@ def test_fp4_decode_split_across_workgroups(dev, M, bps, NKL):
 @pytest.mark.parametrize("MNKB", [(64, 32784, 1792, True), (40, 20480, 2304, False),
                                   (33, 24576, 1280, True)])
 def test_fp4_decode_shared_a(dev, MNKB):
-    """33-64 rows at one slice over wide N: the shared-A variant with 4 groups
-    per wave (N > 32768; 7 steps: a five-step ring and a two-step tail) and 2
-    (9 steps against a seven-step ring; 5 steps, shorter than the ring),
-    MXFP4 operands (one scale dword per step)."""
+    """33-64 rows at one slice over wide N: the shared-A variant with four
+    waves of 4 groups (N > 32768; 7 steps: a five-step ring and a two-step
+    tail) and eight waves of one group (9 steps against an eight-step ring;
+    5 steps, shorter than the ring), MXFP4 operands (one scale dword per
+    step)."""
     M, N, K, bps = MNKB
     qa, sa, qb, sb = mx4_operands(M, N, K, seed=M + K)
     name = ("ga_mxfp4_bf16_BpreShuffle_256x256" if bps else
