@@ -81,6 +81,9 @@ def parse():
     ap.add_argument("--profile-workload", default=None, metavar="NAME",
                     help="counter run: the calibration copies, then --steps calls of one "
                          "workload (" + ", ".join(PROFILE_WORKLOADS) + "), nothing else timed")
+    ap.add_argument("--trace-summary", default=None, metavar="DIR",
+                    help="print the timed launches of every workload in a rocprofv3 "
+                         "--kernel-trace of the bench (DIR/**/*kernel_trace.csv)")
     ap.add_argument("--traffic-summary", default=None, metavar="DIR",
                     help="write profiles/traffic.json from the rocprofv3 counter runs under "
                          "DIR/<workload>/{FETCH_SIZE,WRITE_SIZE}/")
@@ -126,6 +129,7 @@ def mx_problem(torch, ops, f4gemm, M, N, K, b_std=1.0, nsets=1, seed=0, elem_bit
 
 
 WARMUP_S = 0.05
+RUN_GAP_S = 0.002
 
 
 def warm_up(torch, fn, warmup):
@@ -134,7 +138,11 @@ def warm_up(torch, fn, warmup):
     over the first 30-40 ms of load and then holds it (measured on MXFP8
     8192^3: 424 us/launch over the first 50 launches from idle, 389-391 over
     each of the next 450; 4096^3: 64.5 then 56.6-57.3, no decline over 200
-    ms), so every timed region starts from the settled clock."""
+    ms), so every timed region starts from the settled clock. It starts
+    with RUN_GAP_S of idle GPU, which marks each workload's start in a kernel
+    trace (--trace-summary)."""
+    torch.cuda.synchronize()
+    time.sleep(RUN_GAP_S)
     t0 = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t0 < WARMUP_S:
@@ -723,7 +731,8 @@ def traffic_summary(root_dir, calls):
     --profile-workload W --steps calls` (FETCH_SIZE, then WRITE_SIZE, in KiB
     per dispatch). Each counter is scaled by what it reads for the 512 MiB
     device copy (the first two dispatches); a call's traffic is the sum over
-    the workload's library dispatches divided by the number of calls."""
+    the workload's library dispatches divided by the number of calls.
+    Workloads with no counter runs under root_dir keep their entries."""
     import csv
     res = {}
     for wl in sorted(os.listdir(root_dir)):
@@ -772,11 +781,87 @@ def traffic_summary(root_dir, calls):
                                   "-- python3 bench.py --calib-copy --profile-workload %s "
                                   "--steps %d" % (wl, calls)}
     path = os.path.join(ROOT, "profiles", "traffic.json")
+    # workloads without counter runs under root_dir keep their committed entries
+    try:
+        with open(path) as f:
+            kept = json.load(f).get("workloads", {})
+    except (OSError, ValueError):
+        kept = {}
+    kept.update(res)
+    res = kept
     with open(path, "w") as f:
         json.dump({"note": "HBM bytes per call from FETCH_SIZE + WRITE_SIZE, each scaled by its "
                            "reading for a 512 MiB device copy; a split-K call counts its "
                            "reduce", "workloads": res}, f, indent=1, sort_keys=True)
     return path
+
+
+def _trace_kernel(name):
+    """A library kernel's name without namespaces and arguments."""
+    n = name.replace("void ", "").replace("ga::(anonymous namespace)::", "").replace("ga::", "")
+    depth, out = 0, ""
+    for ch in n:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out += ch
+    return out
+
+
+def trace_summary(root_dir, min_gap_ms=1.5, min_launches=30):
+    """Markdown table of a rocprofv3 --kernel-trace of bench.py: the trace is
+    cut at idle gaps of at least min_gap_ms (every workload's warmup starts
+    after RUN_GAP_S of idle GPU); in each piece, the library GEMM or quantiser
+    kernel launched at least min_launches times with one grid is a workload
+    run, its split-K reduce (when it has one) counted beside it. Timed
+    launches: a time_gemm run ends with its 100 timed launches then 10 timed
+    one by one, a time_call run with its timed launches, so the table gives
+    both the mean of launches [-110, -10) and of the last 100, in microseconds
+    (dispatch start to end)."""
+    import csv
+    rows = []
+    for dp, _, files in os.walk(root_dir):
+        for f in files:
+            if f.endswith("kernel_trace.csv"):
+                with open(os.path.join(dp, f)) as fh:
+                    rows += list(csv.DictReader(fh))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    pieces, last = [], None
+    for r in rows:
+        s, e = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if last is None or s - last >= min_gap_ms * 1e6:
+            pieces.append([])
+        pieces[-1].append(r)
+        last = e if last is None else max(last, e)
+    lines = ["| run | kernel | workgroups x threads | launches | timed [-110, -10) us | "
+             "last 100 us | split-K reduce us |", "|---|---|---|---|---|---|---|"]
+    nrun = 0
+    for piece in pieces:
+        groups = {}
+        for r in piece:
+            name = _trace_kernel(r["Kernel_Name"])
+            if "ga::" not in r["Kernel_Name"] or "shuffle" in name:
+                continue
+            wg = int(r["Workgroup_Size_X"])
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            groups.setdefault((name, grid // wg, wg), []).append(
+                int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        main = [(k, d) for k, d in groups.items()
+                if "splitk_reduce" not in k[0] and len(d) >= min_launches]
+        if len(main) != 1:
+            continue
+        (name, nwg, wg), d = main[0]
+        red = [v for k, v in groups.items() if "splitk_reduce" in k[0]]
+        red = red[0] if red else []
+        t110 = d[-110:-10] if len(d) >= 160 else d[-100:]
+        r110 = red[-110:-10] if len(red) >= 160 else red[-100:]
+        nrun += 1
+        lines.append("| %d | `%s` | %d x %d | %d | %.2f | %.2f | %s |" % (
+            nrun, name, nwg, wg, len(d), sum(t110) / len(t110) / 1e3,
+            sum(d[-100:]) / len(d[-100:]) / 1e3,
+            "%.2f" % (sum(r110) / len(r110) / 1e3) if r110 else "-"))
+    return "\n".join(lines)
 
 
 def measured_traffic(workload, kernel=None, log2_k_split=None):
@@ -906,6 +991,9 @@ def main():
     args = parse()
     if args.traffic_summary:
         print(traffic_summary(args.traffic_summary, args.steps))
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
         return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (--gpus %d requested); a sharded run "
