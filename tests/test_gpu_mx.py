@@ -383,8 +383,8 @@ def test_decode_split_across_workgroups(dev, M, bps, NKL):
 
 # 33-64 rows at one slice over wide N: the shared-A variant (A through an LDS
 # ring). (M, N, K, preshuffled B): eight waves of one group (shares of 6, 5
-# and 7 groups: waves without a group) with the ring (8 steps) longer than the
-# slice (5 steps), 33 rows; 9 steps (one pass of the main loop and a one-step
+# and 7 groups: waves without a group) with the ring (6 steps) longer than the
+# slice (5 steps), 33 rows; 9 steps (one pass of the main loop and a three-step
 # tail); 7 groups per workgroup as at N = 28672; four waves of 4 groups (N >
 # 32768: the five-step ring without paired scale loads) over 13 steps (two
 # passes, a three-step tail) and 9, with one workgroup of 9 groups among 8s.

@@ -266,7 +266,7 @@ def test_fp4_decode_split_across_workgroups(dev, M, bps, NKL):
 def test_fp4_decode_shared_a(dev, MNKB):
     """33-64 rows at one slice over wide N: the shared-A variant with four
     waves of 4 groups (N > 32768; 7 steps: a five-step ring and a two-step
-    tail) and eight waves of one group (9 steps against an eight-step ring;
+    tail) and eight waves of one group (9 steps against a six-step ring;
     5 steps, shorter than the ring), MXFP4 operands (one scale dword per
     step)."""
     M, N, K, bps = MNKB
