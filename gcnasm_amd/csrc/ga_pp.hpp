@@ -63,6 +63,10 @@ __device__ __forceinline__ void stage_put(char* smem, int row, int col, uint32_t
 
 // Wave w stores rows 32w .. 32w+31 of the staged tile, two rows (64 lanes x
 // 16 B) per instruction, to dst (the tile's first element, row stride ldd).
+// NT: non-temporal stores. A compile-time choice: LLVM merges a store and a
+// non-temporal store of the same value under a run-time branch and drops the
+// hint.
+template <bool NT = false>
 __device__ __forceinline__ void stage_store(const char* smem, uint16_t* dst, int ldd, int wave,
                                             int lane)
 {
@@ -71,7 +75,11 @@ __device__ __forceinline__ void stage_store(const char* smem, uint16_t* dst, int
     for (int it = 0; it < 16; it++) {
         const int row = wave * 32 + it * 2 + (lane >> 5);
         const v4i d = *(const v4i*)(smem + row * kStagePitch + col * 2);
-        *(v4i*)(dst + (size_t)row * ldd + col) = d;
+        v4i* o = (v4i*)(dst + (size_t)row * ldd + col);
+        if constexpr (NT)
+            __builtin_nontemporal_store(d, o);
+        else
+            *o = d;
     }
 }
 

@@ -34,7 +34,7 @@ namespace {
 using namespace pp;
 using namespace bspp;
 
-template <int MODE, int OUT>
+template <int MODE, int OUT, bool NT>
 __global__ __attribute__((amdgpu_flat_work_group_size(kNT, kNT), amdgpu_waves_per_eu(2, 2)))
 void bs_pp_kernel(ga_opus_gemm_kargs ka)
 {
@@ -272,7 +272,11 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
                 for (int r = 0; r < 16; r++) {
                     const int row = wave * 16 + r;
                     const v4i d = *(const v4i*)(smem + row * kStagePitchF32 + lane * 16);
-                    *(v4i*)(dst + (size_t)row * ldc + lane * 4) = d;
+                    v4i* o = (v4i*)(dst + (size_t)row * ldc + lane * 4);
+                    if constexpr (NT)
+                        __builtin_nontemporal_store(d, o);
+                    else
+                        *o = d;
                 }
             }
         } else {
@@ -292,7 +296,7 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
                                   (q & 1) * 128 + simd * 32 + t * 16 + (lane >> 4) * 4, lo, hi);
                     }
             barrier_lds();
-            stage_store(smem, (uint16_t*)pc + (size_t)m0 * ldc + n0, ldc, wave, lane);
+            stage_store<NT>(smem, (uint16_t*)pc + (size_t)m0 * ldc + n0, ldc, wave, lane);
         }
         return;
     }
@@ -338,11 +342,30 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
     }
 }
 
+// Interior tiles store C with non-temporal stores when C, A and B together
+// exceed 320 MiB, more than the 256 MB memory-side cache holds (measured on
+// MI355X, block scale GROUP_N 128, best of 3 x 100 calls, plain -> non-
+// temporal: fp32 C 16384x16384x2048 672 -> 605 us, 4096x24576x1536 208 ->
+// 191, 8192^3 473 -> 465, 4096x16384x4096 273 -> 271; below the limit they
+// cost 1-3 %: 8192x8192x2048 158 -> 161, 4096x8192x4096 138 -> 140,
+// 4096x7168x2048 73 -> 75, 4096^3 69 -> 71).
+bool bs_pp_nontemporal(const ga_opus_gemm_kargs& ka, int out_dtype)
+{
+    const long long c = (long long)ka.m * ka.n * (out_dtype == GA_DTYPE_F32 ? 4 : 2);
+    const long long ab = (long long)(ka.m + ka.n) * ka.k;
+    return (c + ab) * ka.batch > (320ll << 20);
+}
+
 template <int MODE, int OUT>
 void launch_bs_pp_t(const ga_opus_gemm_kargs& ka, hipStream_t stream)
 {
     const int tn = (ka.n + 255) / 256, tm = (ka.m + 255) / 256;
-    hipLaunchKernelGGL((bs_pp_kernel<MODE, OUT>), dim3(tn, tm, ka.batch), dim3(kNT), 0, stream, ka);
+    if (bs_pp_nontemporal(ka, OUT))
+        hipLaunchKernelGGL((bs_pp_kernel<MODE, OUT, true>), dim3(tn, tm, ka.batch), dim3(kNT), 0,
+                           stream, ka);
+    else
+        hipLaunchKernelGGL((bs_pp_kernel<MODE, OUT, false>), dim3(tn, tm, ka.batch), dim3(kNT), 0,
+                           stream, ka);
 }
 
 } // namespace
