@@ -99,26 +99,40 @@ def test_blockscale(dev, group_n, shape):
     assert_parity(st, "bs bf16 %s g%d" % (shape, group_n))
 
 
-@pytest.mark.parametrize("shape", [(4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)])
-def test_blockscale_deepseek_configs(dev, shape):
-    """The DeepSeek shapes the benchmark configuration names, run whole on the
-    GPU (fp32 and bf16 C) and checked on the first and last 8 rows and one row
-    of every 256-row tile (the CPU oracle on every row would take minutes)."""
+def check_rows_fp32_bf16(dev, shape, group_n, seed):
+    """Runs a whole GEMM on the GPU (fp32 and bf16 C) and checks the first and
+    last 8 rows and one row of every 256-row tile against the oracle (the CPU
+    oracle on every row would take minutes)."""
     M, N, K = shape
-    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=17)
+    qa, qb, sfa, sfb = ds_operands(M, N, K, seed=seed, group_n=group_n)
     rows = np.unique(np.concatenate([np.arange(8), np.arange(M - 8, M), tile_rows(M)]))
     qa_r = np.ascontiguousarray(qa[0][rows])
     sfa_r = np.ascontiguousarray(sfa[0][:, rows])
-    want = expect_bs(qa_r, qb[0], sfa_r, sfb[0], 128, M_full=M)
-    absdot = oracle.blockscale_absdot(qa_r, qb[0], sfa_r, sfb[0], 128)
-    C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, 128)
+    want = expect_bs(qa_r, qb[0], sfa_r, sfb[0], group_n, M_full=M)
+    absdot = oracle.blockscale_absdot(qa_r, qb[0], sfa_r, sfb[0], group_n)
+    C = run_bs(dev, qa, qb, sfa, sfb, torch.float32, group_n)
     ok, st = f32_compare(C[0].cpu().numpy()[rows], want, absdot=absdot)
-    assert_parity(st, "bs f32 %s" % (shape,))
+    assert_parity(st, "bs f32 %s g%d" % (shape, group_n))
     del C
-    Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, 128)
+    Cb = run_bs(dev, qa, qb, sfa, sfb, torch.bfloat16, group_n)
     gb = Cb[0].view(torch.int16).cpu().numpy().view(np.uint16)[rows]
     ok, st = bf16_compare(gb, oracle.to_bf16_bits(want), absdot)
-    assert_parity(st, "bs bf16 %s" % (shape,))
+    assert_parity(st, "bs bf16 %s g%d" % (shape, group_n))
+
+
+@pytest.mark.parametrize("shape", [(4096, 7168, 2048), (4096, 2112, 7168), (4096, 24576, 1536)])
+def test_blockscale_deepseek_configs(dev, shape):
+    """The DeepSeek shapes the benchmark configuration names (4096x24576x1536
+    with fp32 C passes the non-temporal store limit below)."""
+    check_rows_fp32_bf16(dev, shape, 128, 17)
+
+
+@pytest.mark.parametrize("group_n", [128, 1])
+def test_blockscale_nontemporal_stores(dev, group_n):
+    """C, A and B together above 320 MiB: the 256x256 kernel writes its staged
+    C rows with non-temporal stores, bf16 C as well as fp32 (16384 x 12288:
+    384 MiB of bf16 C, 768 MiB of fp32)."""
+    check_rows_fp32_bf16(dev, (16384, 12288, 512), group_n, 23)
 
 
 def _rows_checked(M):
