@@ -274,17 +274,23 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
     // A: lane 16g + r reads row 16i + r, K chunks g and g + 4 of the step
     const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
     if constexpr (LA) {
-        // Copy q = 2s + h of the panel: lane 16g + r copies row r, K chunk
-        // g + 4h of step s (rows past M read as zeros) to LDS byte
-        // q * 1024 + lane * 16, so lane 16g + r's operand of step s is at its
-        // own lane offset in copies 2s and 2s + 1. The waves take the copies
+        // The panel holds step s as 16 rows of 128 bytes at LDS byte s * 2048,
+        // K chunk c of row r at slot c ^ ((r >> 1) & 7). Copy q = 2s + h
+        // writes rows 8h .. 8h + 7 of step s: lane l reads whole 128-byte
+        // lines (row 8h + l / 8, slot l % 8; rows past M read as zeros) to LDS
+        // byte q * 1024 + l * 16. Copies of 16 rows x 64 bytes each (the
+        // earlier form) moved the same bytes slower. The waves take the copies
         // in turn; a wave without columns waits for its own and meets the
         // others at the barrier the working waves take after their prologue.
         const int nw = (int)(blockDim.x >> 6);
         const int ncopies = 2 * (K / (128 * kEPB));
+        const uint32_t crow = (uint32_t)lane >> 3, cslot = lane & 7;
+        const uint32_t cva0 = crow * lda + ((cslot ^ ((crow >> 1) & 7)) * 16) + (uint32_t)kbb;
+        const uint32_t cva1 = (crow + 8) * lda + ((cslot ^ (((crow + 8) >> 1) & 7)) * 16) +
+                              (uint32_t)kbb;
         for (int q = wave; q < ncopies; q += nw)
             lds_load16(ra, (lds_void*)(a_lds + q * 1024),
-                       va + uni((uint32_t)(q >> 1) * 128 + (uint32_t)(q & 1) * 64), 0);
+                       ((q & 1) ? cva1 : cva0) + uni((uint32_t)(q >> 1) * 128), 0);
         __builtin_amdgcn_sched_barrier(0); // the prologue's counted loads follow the copies
         if (nsteps == 0) {
             wait_vmcnt<0>();
@@ -362,12 +368,15 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
                     fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
             }
         };
-        // LA: step s's A fragment from the panel in LDS
+        // LA: step s's A fragment from the panel in LDS: lane 16g + r reads
+        // row r, chunks g and g + 4 (slots g ^ sw and g ^ sw ^ 4, sw =
+        // (r >> 1) & 7: 64 distinct banks per 16 lanes)
+        const uint32_t ao = (uint32_t)r * 128 + ((g ^ ((r >> 1) & 7)) * 16);
         auto read_a = [&](int s, auto J) {
             if constexpr (LA) {
                 constexpr int j = decltype(J)::value;
-                const v4i y0 = *(const v4i*)(a_lds + s * 2048 + lane * 16);
-                const v4i y1 = *(const v4i*)(a_lds + s * 2048 + 1024 + lane * 16);
+                const v4i y0 = *(const v4i*)(a_lds + s * 2048 + ao);
+                const v4i y1 = *(const v4i*)(a_lds + s * 2048 + (ao ^ 64u));
                 fa[j][0] = (v8i){y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
             }
         };
@@ -697,11 +706,15 @@ __global__ __launch_bounds__(64 * W) void mx_decode_la_kernel(ga_f4gemm_kargs ar
         const uint32_t lda = args.stride_A0 / kEPB; // bytes
         const long long abytes = (long long)M * lda;
         const auto ra = make_rsrc(args.ptr_A, (uint32_t)(abytes > 0xFFFFFFF0ll ? 0xFFFFFFF0ll : abytes));
-        // A copy (i, h) of a step: lane 16g + r copies row 16i + r, K chunk
-        // g + 4h, to LDS byte lane * 16 of the copy's 1 KB; the MFMA operand
-        // of lane 16g + r is chunks g and g + 4 of row 16i + r: copies (i, 0)
-        // and (i, 1) at the same lane offset
-        const uint32_t va = (uint32_t)r * lda + g * 16 + (uint32_t)kbb;
+        // A of a step in LDS: rows 16i .. 16i + 15 as 128-byte rows at byte
+        // i * 2048 of the slot, K chunk c of row 16i + t at slot
+        // c ^ ((t >> 1) & 7). Copy (i, h) writes rows 16i + 8h .. + 7 from
+        // whole 128-byte lines (lane l: row 16i + 8h + l / 8, slot l % 8) to
+        // LDS byte (2i + h) * 1024 + l * 16.
+        const uint32_t crow = (uint32_t)lane >> 3, cslot = lane & 7;
+        const uint32_t cva0 = crow * lda + ((cslot ^ ((crow >> 1) & 7)) * 16) + (uint32_t)kbb;
+        const uint32_t cva1 = (crow + 8) * lda + ((cslot ^ (((crow + 8) >> 1) & 7)) * 16) +
+                              (uint32_t)kbb;
         __amdgpu_buffer_rsrc_t rbuf;
         uint32_t vb, b_step, b_hi, b_grp;
         const int ngb = live ? ng_here : 0;
@@ -740,7 +753,7 @@ __global__ __launch_bounds__(64 * W) void mx_decode_la_kernel(ga_f4gemm_kargs ar
             for (int e = 0; e < BPW; e++) {
                 const int bi = wave * BPW + e, i = bi >> 1, h = bi & 1;
                 lds_load16(ra, (lds_void*)(smem + slot * kSlot + bi * 1024),
-                           va + uni((uint32_t)s * 128 + (uint32_t)i * 16 * lda + (uint32_t)h * 64), 0);
+                           (h ? cva1 : cva0) + uni((uint32_t)s * 128 + (uint32_t)i * 16 * lda), 0);
             }
         };
         auto load_bs = [&](int s, auto J) {
@@ -762,14 +775,17 @@ __global__ __launch_bounds__(64 * W) void mx_decode_la_kernel(ga_f4gemm_kargs ar
                     fsb[j][c] = buf_load4(rsb, vsb[c] + uni(q), 0);
             }
         };
-        // step in slot j: A operand of rows 16i .. 16i + 15 from copies (i, 0), (i, 1)
+        // step in slot j: A operand of rows 16i .. 16i + 15, lane 16g + r
+        // reading row 16i + r, chunks g and g + 4 (64 distinct banks per 16
+        // lanes)
         v8i fa[TM];
+        const uint32_t ao = (uint32_t)r * 128 + ((g ^ ((r >> 1) & 7)) * 16);
         auto read_a = [&](int j) {
-            const char* pa = smem + j * kSlot + lane * 16;
+            const char* pa = smem + j * kSlot;
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                const v4i x0 = *(const v4i*)(pa + (2 * i) * 1024);
-                const v4i x1 = *(const v4i*)(pa + (2 * i + 1) * 1024);
+                const v4i x0 = *(const v4i*)(pa + i * 2048 + ao);
+                const v4i x1 = *(const v4i*)(pa + i * 2048 + (ao ^ 64u));
                 fa[i] = (v8i){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
             }
         };
