@@ -278,8 +278,8 @@ void mx_decode_kernel(ga_f4gemm_kargs args, int nwg, int ks, float* __restrict__
         // K chunk c of row r at slot c ^ ((r >> 1) & 7). Copy q = 2s + h
         // writes rows 8h .. 8h + 7 of step s: lane l reads whole 128-byte
         // lines (row 8h + l / 8, slot l % 8; rows past M read as zeros) to LDS
-        // byte q * 1024 + l * 16. Copies of 16 rows x 64 bytes each (the
-        // earlier form) moved the same bytes slower. The waves take the copies
+        // byte q * 1024 + l * 16 (copies of 16 rows x 64 bytes per
+        // instruction move the same bytes slower). The waves take the copies
         // in turn; a wave without columns waits for its own and meets the
         // others at the barrier the working waves take after their prologue.
         const int nw = (int)(blockDim.x >> 6);
