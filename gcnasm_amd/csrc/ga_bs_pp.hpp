@@ -154,7 +154,10 @@ __device__ __forceinline__ void apply_scales_t1(const ScaleVals& v, v4f (&acc)[4
 // p[i][t] is folded into its accumulator (acc += p * SFA*SFB): the VALU work
 // of a tile issues while the MFMA pipe runs the previous tile's MFMA. With
 // SPLIT only the t = 0 tiles are folded here; the memory slot before this
-// one folded the t = 1 tiles (BS_MEM_SLOT_SPLIT).
+// one folded the t = 1 tiles (BS_MEM_SLOT_SPLIT). The B tiles alternate
+// direction from one A tile to the next, so consecutive MFMAs differ in one
+// operand (fewer operand bits change in the MFMA pipe; every tile's fold
+// still comes just before its own MFMA).
 template <int MODE, bool APPLY, bool SPLIT = false>
 __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], v4f (&p)[4][2], const v8i (&a)[4],
                                              const v8i (&b)[2], v4f (&acc_prev)[4][2],
@@ -165,7 +168,7 @@ __device__ __forceinline__ void mma_quadrant(v4f (&acc)[4][2], v4f (&p)[4][2], c
     static_for<4>([&](auto I) {
         constexpr int i = decltype(I)::value;
         static_for<2>([&](auto T) {
-            constexpr int t = decltype(T)::value;
+            constexpr int t = (i & 1) ? 1 - decltype(T)::value : decltype(T)::value;
             constexpr bool fold = APPLY && !(SPLIT && t == 1);
             if constexpr (MODE == PS_TENSOR) {
                 acc[i][t] = mfma_mx16<0, 0>(b[t], a[i], acc[i][t], 127, 127);
