@@ -168,8 +168,10 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
         // group, in the same order, as the unsplit fold.
         ScaleVals svn = {};
         sv = svn;
-        for (int s = 0; s < nsteps; s++) {
-            const int slot = s & 1;
+        // two K groups per iteration: the LDS slot is a compile-time read
+        // offset instead of a VALU add per read base
+        auto group = [&](int s, auto SLOT) {
+            constexpr int slot = decltype(SLOT)::value;
             const int r0 = s & 3, r2 = (s + 2) & 3;
             // phase 1 (folds in quadrant 11 of the previous group)
             BS_MEM_SLOT_SPLIT(0, 0, r0, issue_a(L, smem, 1, s + 1, wave),
@@ -196,13 +198,20 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
                               read_b<0>(rb, slot ^ 1, fb0), 10 + S, acc[2], true);
             mma_quadrant<MODE, true, true>(acc[3], p, fa, fb1, acc[2], sv);
             slot_sync();
+        };
+        int s = 0;
+        for (; s + 1 < nsteps; s += 2) {
+            group(s, std::integral_constant<int, 0>{});
+            group(s + 1, std::integral_constant<int, 1>{});
         }
+        if (s < nsteps)
+            group(s, std::integral_constant<int, 0>{});
         if (grp == 0)
             slot_sync(); // matches the second group's extra barrier
         apply_scales<MODE>(svn, acc[3], p);
     } else {
-        for (int s = 0; s < nsteps; s++) {
-            const int slot = s & 1;
+        auto group = [&](int s, auto SLOT) {
+            constexpr int slot = decltype(SLOT)::value;
             const int r0 = s & 3, r2 = (s + 2) & 3, rprev = (s - 1) & 3;
             // phase 1 (folds in quadrant 11 of the previous group)
             BS_MEM_SLOT(1, 1, rprev, issue_a(L, smem, 1, s + 1, wave), read_a<0>(rb, slot, fa),
@@ -228,7 +237,14 @@ void bs_pp_kernel(ga_opus_gemm_kargs ka)
                         10 + S);
             mma_quadrant<MODE, true>(acc[3], p, fa, fb1, acc[2], sv);
             slot_sync();
+        };
+        int s = 0;
+        for (; s + 1 < nsteps; s += 2) {
+            group(s, std::integral_constant<int, 0>{});
+            group(s + 1, std::integral_constant<int, 1>{});
         }
+        if (s < nsteps)
+            group(s, std::integral_constant<int, 0>{});
         if (grp == 0)
             slot_sync(); // matches the second group's extra barrier
         const ScaleVals last = read_scales<MODE, 1, 1>(rb, (nsteps - 1) & 3);

@@ -432,35 +432,45 @@ __device__ __forceinline__ void pp_tile(const PpArgs& args, float* __restrict__ 
                 if (s + 1 < nsteps)
                     step(s + 1, std::integral_constant<int, 1>{});
             }
-        } else
-        for (int s = 0; s < nsteps; s++) {
-            // MXFP4: one ring slot per step
-            const int P = s & 1;
-            const int r1 = r0 == 2 ? 0 : r0 + 1; // slot of step s + 1
-            const int r2 = r0 == 0 ? 2 : r0 - 1; // (r0 + 2) % 3
-            // X
-            issue_a(L, smem, 1, s + 1, wave);
-            read_sa<0, FP4>(rb, r0, 0u, sa);
-            sb0 = read_sb<0, FP4>(rb, r0, 0u);
-            sb1 = read_sb<1, FP4>(rb, r0, 0u);
-            read_a<0>(rb, P, fa);
-            read_b<0>(rb, P, fb0);
-            read_b<1>(rb, P, fb1);
-            part_sync<8 + kS>();
-            mma_two<FP4, F>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
-            part_sync<8 + kS>();
-            // Y
-            issue_a(L, smem, 0, s + 2, wave);
-            issue_b(L, smem, 0, s + 2, wave);
-            issue_b(L, smem, 1, s + 2, wave);
-            issue_s(L, smem, s + 2, 0, r2, wave);
-            issue_s(L, smem, s + 2, 1, r2, wave);
-            read_sa<1, FP4>(rb, r0, 0u, sa);
-            read_a<1>(rb, P, fa);
-            part_sync<8 + kS>();
-            mma_two<FP4, F>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
-            part_sync<8 + kS>();
-            r0 = r1;
+        } else {
+            // MXFP4: one ring slot per step; two steps per iteration, so the
+            // LDS slot P is a compile-time read offset (no VALU add per read
+            // base)
+            auto step4 = [&](int s, auto PC) {
+                constexpr int P = decltype(PC)::value;
+                const int r1 = r0 == 2 ? 0 : r0 + 1; // slot of step s + 1
+                const int r2 = r0 == 0 ? 2 : r0 - 1; // (r0 + 2) % 3
+                // X
+                issue_a(L, smem, 1, s + 1, wave);
+                read_sa<0, FP4>(rb, r0, 0u, sa);
+                sb0 = read_sb<0, FP4>(rb, r0, 0u);
+                sb1 = read_sb<1, FP4>(rb, r0, 0u);
+                read_a<0>(rb, P, fa);
+                read_b<0>(rb, P, fb0);
+                read_b<1>(rb, P, fb1);
+                part_sync<8 + kS>();
+                mma_two<FP4, F>(acc[0], acc[1], fa, fb0, fb1, sa, sb0, sb1);
+                part_sync<8 + kS>();
+                // Y
+                issue_a(L, smem, 0, s + 2, wave);
+                issue_b(L, smem, 0, s + 2, wave);
+                issue_b(L, smem, 1, s + 2, wave);
+                issue_s(L, smem, s + 2, 0, r2, wave);
+                issue_s(L, smem, s + 2, 1, r2, wave);
+                read_sa<1, FP4>(rb, r0, 0u, sa);
+                read_a<1>(rb, P, fa);
+                part_sync<8 + kS>();
+                mma_two<FP4, F>(acc[2], acc[3], fa, fb0, fb1, sa, sb0, sb1);
+                part_sync<8 + kS>();
+                r0 = r1;
+            };
+            int s = 0;
+            for (; s + 1 < nsteps; s += 2) {
+                step4(s, std::integral_constant<int, 0>{});
+                step4(s + 1, std::integral_constant<int, 1>{});
+            }
+            if (s < nsteps)
+                step4(s, std::integral_constant<int, 0>{});
         }
         if (grp == 0)
             slot_sync(); // matches the second group's extra barrier
