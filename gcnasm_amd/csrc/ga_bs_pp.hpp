@@ -31,28 +31,33 @@ struct BsLoad {
     uint32_t s_kstep;                  // scale bytes per K group
 };
 
+// The copies take their wave-uniform offsets in the SGPR soffset: the
+// VALU adds they cost as VGPR offsets sit in a loop whose time is VALU and
+// MFMA issue (block scale 8192^3 on the reference driver's data 440.6 ->
+// 437.4 us, 4096x2112x7168 77.6 -> 76.6 us on one box; the MXFP8 and MXFP4
+// kernel ran slower that way and keeps VGPR offsets).
 __device__ __forceinline__ void issue_a(const BsLoad& L, char* smem, int h, int t, int wave)
 {
     char* dst = smem + kARegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
     const uint32_t o = (uint32_t)h * 2 * L.a_hstep + (uint32_t)t * 128;
-    lds_load16(L.ra, (lds_void*)dst, L.va + uni(o), 0);
-    lds_load16(L.ra, (lds_void*)(dst + 8192), L.va + uni(o + L.a_hstep), 0);
+    lds_load16(L.ra, (lds_void*)dst, L.va, uni(o));
+    lds_load16(L.ra, (lds_void*)(dst + 8192), L.va, uni(o + L.a_hstep));
 }
 
 __device__ __forceinline__ void issue_b(const BsLoad& L, char* smem, int h, int t, int wave)
 {
     char* dst = smem + kBRegion + (t & 1) * kOpSlot + h * kHalf + wave * 1024;
     const uint32_t o = (uint32_t)h * 2 * L.b_hstep + (uint32_t)t * 128;
-    lds_load16(L.rb, (lds_void*)dst, L.vb + uni(o), 0);
-    lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb + uni(o + L.b_hstep), 0);
+    lds_load16(L.rb, (lds_void*)dst, L.vb, uni(o));
+    lds_load16(L.rb, (lds_void*)(dst + 8192), L.vb, uni(o + L.b_hstep));
 }
 
 // Scales of K group t into ring slot `ring`: one 4-byte copy per lane.
 __device__ __forceinline__ void issue_s(const BsLoad& L, char* smem, int t, int ring, int wave)
 {
     char* dst = smem + kSBase + ring * kSSlot + wave * 256;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4,
-                                             L.vs + uni((uint32_t)t * L.s_kstep), 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)dst, 4, L.vs,
+                                             uni((uint32_t)t * L.s_kstep), 0, 0);
 }
 
 struct BsRead {

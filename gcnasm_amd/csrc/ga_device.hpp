@@ -65,7 +65,10 @@ __device__ __forceinline__ float* resolve_ws(const ga_splitk_ws_handle* h, uint3
 }
 
 // 16 bytes per lane from buffer `r` at byte offset voff+soff into LDS at
-// lds_base + lane*16 (lds_base wave-uniform; M0 takes it).
+// lds_base + lane*16 (lds_base wave-uniform; M0 takes it). The range check
+// covers voff + soff (checked on MI355X: lanes whose voff alone is in range
+// but voff + soff is not read zeros), so a wave-uniform part of the offset
+// can go in soff without a VALU add.
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, lds_void* lds_base,
                                            uint32_t voff, uint32_t soff)
 {
